@@ -1,0 +1,99 @@
+/* vaayu_amd: packed-expert routed-MoE kernels for MI355X (gfx950), C ABI.
+ *
+ * Every entry point takes raw device pointers (the caller owns all memory, e.g. torch
+ * tensors' data_ptr()), plain sizes, dtype codes and a hipStream_t passed as void*. No
+ * entry point allocates device memory, synchronises, or calls back into the host: each
+ * enqueues kernels on `stream` and returns, so a caller may record them into a HIP graph.
+ *
+ * Return value: 0 on success; a negative value for a rejected call (bad argument, or a
+ * geometry the kernels do not take), with the reason in vaayu_last_error(); a positive
+ * value is the hipError_t of a failed launch.
+ *
+ * dtype codes are the reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70):
+ * 0 = bfloat16, 1 = float16, 2 = float32.
+ */
+#ifndef VAAYU_AMD_H
+#define VAAYU_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VAAYU_ABI_VERSION 1
+
+enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
+
+/* One packed expert blob's geometry: `geom = (bits, group, roles)` and the per-role
+ * (word offset, scale offset) that `_layout` derives from it
+ * (vaayu/packed_expert_kernels.py:301-309). gate/up are [inter, hidden], down is
+ * [hidden, inter], codes packed along the last dim. */
+typedef struct vaayu_geom {
+    int32_t bits;      /* code width: 1, 2, 4 or 8 */
+    int32_t group;     /* codes per scale along a row */
+    int32_t hidden;    /* H */
+    int32_t inter;     /* I */
+    int64_t gate_w, gate_s;
+    int64_t up_w, up_s;
+    int64_t down_w, down_s;
+} vaayu_geom;
+
+int vaayu_abi_version(void);
+const char *vaayu_last_error(void);
+
+/* Decode, gate/up stage. Replaces `_gate_up` / `_gate_up_kernel`
+ * (vaayu/packed_expert_kernels.py:355-371, 131-150).
+ * x      [hidden] activations (dtype `act`)
+ * table  int64 [n_pairs * 3]: (packed address, scale address, slot) per pair -- the
+ *        reference's `_table_values` (:349-352), on the device
+ * h      [n_pairs, inter] (dtype `act`) <- round(SiLU(round(x.Wg))) * round(x.Wu), rounded */
+int vaayu_decode_gate_up(const void *x, const int64_t *table, void *h, int32_t n_pairs,
+                         const vaayu_geom *geom, int32_t act, int32_t scale_dtype, void *stream);
+
+/* Decode, down stage and the fixed-order sum. Replaces `_down` / `_down_kernel`
+ * (vaayu/packed_expert_kernels.py:374-387, 153-176).
+ * out [hidden] fp32, OVERWRITTEN with the sum over pairs in table order of
+ * fl32(round(h[p].Wd) * routing_weights[slot_p]), rounded again when w_round != 0
+ * (routing weights already in the activation dtype). */
+int vaayu_decode_down(const void *h, const int64_t *table, const void *routing_weights,
+                      int32_t rw_dtype, float *out, int32_t n_pairs, const vaayu_geom *geom,
+                      int32_t act, int32_t scale_dtype, int32_t w_round, void *stream);
+
+/* Prefill, gate/up stage over 16-row blocks of one expert each. Replaces `_gate_up_g` /
+ * `_gate_up_grouped` (vaayu/packed_expert_kernels.py:720-732, 179-215).
+ * x     [tokens, hidden] contiguous (dtype `act`: bf16 or fp16)
+ * rows  int64 [n_blocks * 16]: row ids token*top_k + slot, -1 pads a block
+ * table int64 [n_blocks * 2]: (packed address, scale address) of each block's expert
+ * h     [tokens * top_k, inter] (dtype `act`); padding rows are never written */
+int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *table, void *h,
+                          int32_t n_blocks, int32_t top_k, const vaayu_geom *geom, int32_t act,
+                          int32_t scale_dtype, void *stream);
+
+/* Prefill, down stage. Replaces `_down_g` / `_down_grouped`
+ * (vaayu/packed_expert_kernels.py:735-749, 218-247).
+ * y [tokens * top_k, hidden] fp32 <- fl32(round(h[row].Wd) * routing_weights[row]),
+ * rounded again when w_round != 0; routing_weights contiguous [tokens * top_k]. */
+int vaayu_prefill_down(const void *h, const int64_t *rows, const int64_t *table,
+                       const void *routing_weights, int32_t rw_dtype, float *y,
+                       int32_t n_blocks, const vaayu_geom *geom, int32_t act,
+                       int32_t scale_dtype, int32_t w_round, void *stream);
+
+/* Prefill reduce. Replaces `_reduce` / `_reduce_kernel` (vaayu/packed_expert_kernels.py:752-757,
+ * 250-260): out[t] = sum over k, in `order`'s order, of y[order[t*top_k + k]], fp32 from 0.
+ * out [tokens, hidden] contiguous fp32, overwritten. */
+int vaayu_prefill_reduce(const float *y, const int64_t *order, float *out, int32_t tokens,
+                         int32_t top_k, int32_t hidden, void *stream);
+
+/* Whole-blob dequant. Replaces `_fused_dequant_kernel` (vaayu/moe_patch.py:750-769), the
+ * function `dequantize_expert_blob` (:849-868) runs: out[i] = round_out((code_i -
+ * 2^(bits-1)) * round_out(scale[i / group])) over n_words * 32/bits codes, bit-exact. */
+int vaayu_dequant_blob(const int32_t *packed, const void *scale, int32_t scale_dtype, void *out,
+                       int32_t out_dtype, int64_t n_words, int32_t bits, int32_t group,
+                       void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VAAYU_AMD_H */

@@ -1,0 +1,44 @@
+"""The whole-blob dequant kernel: bit-exact with the oracle and the eager arithmetic."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import cpu_blobs, to_device
+from vaayu_amd import moe_patch as mp
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 128), (8, 64), (2, 64), (1, 128)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequant_is_bit_exact(bits, gs, out_dtype, sdt):
+    (blob,) = cpu_blobs(512, 256, bits, gs, 1, scale_dtype=sdt)
+    g = to_device(blob)
+    got = mp._hip_dequant(g["flat"]["packed"], g["flat"]["scale"], bits, gs, out_dtype)
+    want = O.dequant_flat(blob["flat"]["packed"], blob["flat"]["scale"], bits, gs, out_dtype)
+    assert np.array_equal(got.float().cpu().numpy(), want)
+    eager = mp._fused_dequant_kernel(g["flat"]["packed"], g["flat"]["scale"], bits, gs, out_dtype)
+    assert torch.equal(got, eager)
+
+
+def test_the_blob_path_uses_the_kernel_and_slices_roles():
+    (blob,) = cpu_blobs(2048, 768, 4, 128, 1, scale_dtype=torch.float16)
+    g = to_device(blob)
+    assert mp._fused_dequant_fn(4, 128, torch.bfloat16, "cuda") is mp._hip_dequant
+    dense = mp.dequantize_expert_blob(g, torch.bfloat16)
+    wg, wd, wu = O.expert_weights(blob, "bf16")
+    for t, o in ((dense["gate"], wg), (dense["down"], wd), (dense["up"], wu)):
+        assert np.array_equal(t.float().cpu().numpy(), o)
+
+
+def test_odd_word_counts_and_tails():
+    rng = np.random.default_rng(0)
+    for n_words in (1, 3, 5, 257):
+        words = torch.from_numpy(rng.integers(-2 ** 31, 2 ** 31, n_words, dtype=np.int64)
+                                 .astype(np.int32)).cuda()
+        scale = torch.from_numpy(rng.uniform(0.001, 0.1, n_words).astype(np.float32)).half().cuda()
+        got = mp._hip_dequant(words, scale, 4, 8, torch.bfloat16)
+        want = O.dequant_flat(words.cpu(), scale.cpu(), 4, 8, "bf16")
+        assert np.array_equal(got.float().cpu().numpy(), want)

@@ -1,0 +1,282 @@
+"""The grouped prefill kernels (HIP MFMA, gfx950) against the oracle.
+
+Ports the reference's tests/test_packed_prefill_kernels.py with the CPU oracle's
+correctly rounded replay as the truth: per-stage rounding, the exact contribution and
+expert-id-order sum, batch invariance, block boundaries, padding, strided views, NaN
+isolation, freed blobs, verdicts.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import vaayu_amd.packed_expert_kernels as pk
+from oracle import oracle as O
+from tests.helpers import frac_equal, gpu_blobs, prefill_case, rel
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+GEOMS = [
+    pytest.param(2048, 512, 4, 32, id="qwen3next-int4-g32"),
+    pytest.param(3072, 1536, 8, 128, id="minimax-dims-int8-g128"),
+    pytest.param(1024, 512, 8, 64, id="int8-g64"),
+    pytest.param(2048, 768, 4, 128, id="qwen3-30b-a3b-int4-g128"),
+]
+QWEN = (2048, 512, 4, 32)
+
+
+def _launch(x, eidx, w, blobs):
+    out = torch.full(x.shape, float("nan"), device="cuda")
+    pk._prefill_launch(x, eidx, w, blobs, out)
+    torch.cuda.synchronize()
+    return out
+
+
+def _stock(x, eidx, w, blobs, linear=F.linear):
+    out = torch.full(x.shape, float("nan"), device="cuda")
+    pk.stock_experts_prefill(x, eidx, w, blobs, out, F.silu, linear=linear)
+    return out
+
+
+def _prefill(x, eidx, w, blobs):
+    out = torch.full(x.shape, float("nan"), device="cuda")
+    pk.packed_experts_prefill(x, eidx, w, blobs, out, F.silu)
+    torch.cuda.synchronize()
+    return out
+
+
+def _stages(x, eidx, w, blobs, h=None, y=None):
+    plan = pk._prefill_plan(eidx)
+    blob = blobs[int(plan[1][0])]
+    geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
+    top_k = eidx.shape[1]
+    tbl, rows, order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=h)
+    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, y=y)
+    torch.cuda.synchronize()
+    return h, y, order, plan
+
+
+@pytest.mark.parametrize("hid,inter,bits,gs", GEOMS)
+def test_each_stage_is_correctly_rounded(hid, inter, bits, gs):
+    """h vs the oracle's correctly rounded stages; y (weight 1) vs the oracle's rounded
+    down output of the kernel's own h: >= 99 % bit-equal each."""
+    x, eidx, w, blobs, cblobs = prefill_case(hid, inter, bits, gs)
+    h, y, _order, _plan = _stages(x, eidx, torch.ones_like(w), blobs)
+    want_h, _y = O.prefill_stages(x, eidx, cblobs)
+    assert frac_equal(h, want_h) >= 0.99, "gate/up/SiLU/product stage"
+    # down of the kernel's own h, correctly rounded
+    hv = O.to_np(h)
+    e = eidx.reshape(-1).numpy()
+    want_y = np.empty((e.size, hid), np.float32)
+    for ex in np.unique(e):
+        rows = np.nonzero(e == ex)[0]
+        _wg, wd, _wu = O.expert_weights(cblobs[int(ex)], "bf16")
+        want_y[rows] = O._linear(hv[rows], wd, "bf16")
+    assert frac_equal(y, want_y) >= 0.99, "down stage"
+
+
+@pytest.mark.parametrize("w_dtype", [torch.float32, BF], ids=["fp32-w", "bf16-w"])
+def test_the_contribution_is_the_rounded_down_output_times_its_weight(w_dtype):
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, w_dtype=w_dtype)
+    _h, down, _o, _p = _stages(x, eidx, torch.ones_like(w), blobs)
+    _h, y, _o, _p = _stages(x, eidx, w, blobs)
+    assert torch.equal(y, (down.to(BF) * w.reshape(-1, 1)).float())
+
+
+@pytest.mark.parametrize("hid,inter,bits,gs", GEOMS)
+def test_the_token_sum_runs_in_expert_id_order(hid, inter, bits, gs):
+    x, eidx, w, blobs, _c = prefill_case(hid, inter, bits, gs)
+    _h, y, order, plan = _stages(x, eidx, w, blobs)
+    out = torch.full(x.shape, float("nan"), device="cuda")
+    pk._reduce(y, order, out, eidx.shape[1])
+    torch.cuda.synchronize()
+    want = O.reduce_in_order(O.to_np(y), O.to_np(order), x.shape[0], eidx.shape[1])
+    assert np.array_equal(O.to_np(out), want)
+
+
+@pytest.mark.parametrize("hid,inter,bits,gs", GEOMS)
+def test_kernel_output_is_as_accurate_as_the_stock_arithmetic(hid, inter, bits, gs):
+    x, eidx, w, blobs, cblobs = prefill_case(hid, inter, bits, gs)
+    got = _launch(x, eidx, w, blobs)
+    precise = O.stock_prefill(x, eidx, w, cblobs)
+    assert rel(got, precise) <= 2e-3, f"relL2 vs the oracle {rel(got, precise):.2e}"
+    assert np.abs(O.to_np(got) - precise).max() <= 2e-2
+    assert rel(got, _stock(x, eidx, w, blobs)) <= 1e-2
+
+
+def test_a_token_does_not_depend_on_the_tokens_it_shares_a_call_with():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, tokens=40)
+    full = _launch(x, eidx, w, blobs)
+    for t in (0, 17, 39):
+        alone = _launch(x[t:t + 1], eidx[t:t + 1], w[t:t + 1], blobs)
+        assert torch.equal(alone[0], full[t]), f"token {t}"
+
+
+def test_block_boundaries():
+    counts = {1: 1, 4: 16, 7: 17, 10: 40}
+    slots = [e for e, c in counts.items() for _ in range(c)]
+    filler = [13, 16, 19, 22]
+    eidx = torch.tensor([[e, filler[i % 4]] for i, e in enumerate(slots)])
+    x, eidx, w, blobs, cblobs = prefill_case(*QWEN, top_k=2, eidx=eidx)
+    plan = pk._prefill_plan(eidx)
+    assert [int(c) for c in plan[2][:4]] == [1, 16, 17, 40]
+    full = _launch(x, eidx, w, blobs)
+    assert not torch.isnan(full).any()
+    for t in (0, 1, 16, 17, 33, 34, 73):
+        alone = _launch(x[t:t + 1], eidx[t:t + 1], w[t:t + 1], blobs)
+        assert torch.equal(alone[0], full[t]), f"token {t}"
+    assert rel(full, O.stock_prefill(x, eidx, w, cblobs)) <= 2e-3
+
+
+def test_padding_rows_are_never_written():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, tokens=5, top_k=3)
+    n, inter, hid = eidx.numel(), QWEN[1], QWEN[0]
+    h_big = torch.full((n + 2, inter), 7.0, dtype=BF, device="cuda")
+    y_big = torch.full((n + 2, hid), 7.0, device="cuda")
+    _stages(x, eidx, w, blobs, h=h_big[1:n + 1], y=y_big[1:n + 1])
+    for big in (h_big, y_big):
+        assert (big[0] == 7.0).all() and (big[-1] == 7.0).all(), "a guard row was written"
+        assert not (big[1:n + 1] == 7.0).all(dim=1).any(), "a live row was not written"
+
+
+def test_the_output_does_not_depend_on_where_the_blobs_live_or_their_order():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    moved = {e: {"flat": {n: t.clone() for n, t in b["flat"].items()}, "geom": b["geom"]}
+             for e, b in reversed(list(blobs.items()))}
+    assert torch.equal(_launch(x, eidx, w, blobs), _launch(x, eidx, w, moved))
+
+
+def test_a_zero_weight_duplicate_slot_changes_nothing():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    eidx2 = torch.cat([eidx, eidx[:, :1]], dim=1)
+    w2 = torch.cat([w, torch.zeros_like(w[:, :1])], dim=1)
+    assert torch.equal(_launch(x, eidx, w, blobs), _launch(x, eidx2, w2, blobs))
+
+
+def test_one_token():
+    x, eidx, w, blobs, cblobs = prefill_case(*QWEN, tokens=1)
+    assert rel(_launch(x, eidx, w, blobs), O.stock_prefill(x, eidx, w, cblobs)) <= 2e-3
+
+
+def test_a_nan_token_poisons_its_own_row_and_no_other():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    clean = _launch(x, eidx, w, blobs)
+    x = x.clone()
+    x[0, 5] = float("nan")
+    got = _launch(x, eidx, w, blobs)
+    assert torch.isnan(got[0]).all()
+    assert torch.equal(got[1:], clean[1:])
+
+
+def test_a_strided_view_of_the_activations_is_read_as_what_it_holds():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    wide = torch.zeros(2 * x.shape[0], x.shape[1], dtype=BF, device="cuda")
+    wide[::2] = x
+    view = wide[::2]
+    assert not view.is_contiguous()
+    assert torch.equal(_launch(view, eidx, w, blobs), _launch(x, eidx, w, blobs))
+
+
+def test_the_blobs_may_be_freed_as_soon_as_the_launch_returns():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    expected = _launch(x, eidx, w, blobs)
+    mine = {e: {"flat": {n: t.clone() for n, t in b["flat"].items()}, "geom": b["geom"]}
+            for e, b in blobs.items()}
+    sizes = [(t.shape, t.dtype) for b in mine.values() for t in b["flat"].values()]
+    out = torch.empty(x.shape, device="cuda")
+    pk._prefill_launch(x, eidx, w, mine, out)
+    del mine
+    junk = [torch.zeros(shape, dtype=dtype, device="cuda") for shape, dtype in sizes]
+    torch.cuda.synchronize()
+    assert torch.equal(out, expected)
+    assert len(junk) == len(sizes)
+
+
+def test_two_geometries_get_two_verdicts(monkeypatch):
+    monkeypatch.setattr(pk, "_PF_VERDICTS", {})
+    for geom in (QWEN, (1024, 512, 8, 64)):
+        x, eidx, w, blobs, cblobs = prefill_case(*geom)
+        assert rel(_prefill(x, eidx, w, blobs), O.stock_prefill(x, eidx, w, cblobs)) <= 2e-3
+    assert len(pk._PF_VERDICTS) == 2 and all(pk._PF_VERDICTS.values())
+
+
+def test_back_to_back_calls_do_not_share_a_table():
+    cases = [prefill_case(*QWEN, tokens=5 + 3 * s, seed=s)
+             for s in range(3 * len(pk._PF_TABLES._slots))]
+    outs = []
+    for x, eidx, w, blobs, _c in cases:
+        out = torch.empty(x.shape, device="cuda")
+        pk._prefill_launch(x, eidx, w, blobs, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    for (x, eidx, w, blobs, _c), out in zip(cases, outs):
+        assert torch.equal(out, _launch(x, eidx, w, blobs))
+
+
+def test_prefill_uses_the_kernels_when_they_agree(monkeypatch):
+    monkeypatch.setattr(pk, "_PF_VERDICTS", {})
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    assert torch.equal(_prefill(x, eidx, w, blobs), _launch(x, eidx, w, blobs))
+    assert list(pk._PF_VERDICTS.values()) == [True]
+
+
+def test_a_wrong_kernel_is_refused_loudly(monkeypatch, capsys):
+    monkeypatch.setattr(pk, "_PF_VERDICTS", {})
+    monkeypatch.setattr(pk, "_prefill_launch", lambda x, e, w, b, out, plan=None: out.zero_())
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    got = _prefill(x, eidx, w, blobs)
+    assert "WARNING" in capsys.readouterr().out
+    assert torch.equal(got, _stock(x, eidx, w, blobs))
+
+
+def test_a_geometry_with_no_matrix_core_tile_stays_on_the_stock_loop(monkeypatch, capsys):
+    monkeypatch.setattr(pk, "_PF_VERDICTS", {})
+    x, eidx, w, blobs, _c = prefill_case(64, 64, 4, 32, n_exp=8, top_k=2)
+    got = _prefill(x, eidx, w, blobs)
+    out = capsys.readouterr().out
+    assert "WARNING" in out and "K tile" in out
+    assert torch.equal(got, _stock(x, eidx, w, blobs))
+
+
+def test_a_call_the_kernels_cannot_take_runs_the_stock_arithmetic(monkeypatch, capsys):
+    from vaayu_amd.moe_patch import expert_weights_from_entry
+    monkeypatch.setattr(pk, "_PF_VERDICTS", {})
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    first = int(eidx[0, 0])
+    dense = {"dense": dict(zip(("gate", "down", "up"),
+                               expert_weights_from_entry(blobs[first], BF)))}
+    other = gpu_blobs(2048, 512, 4, 64, 1)[0]
+    missing = {e: b for e, b in blobs.items() if e != first}
+    for mixed in ({**blobs, first: dense}, {**blobs, first: other}, missing):
+        assert torch.equal(_prefill(x, eidx, w, mixed), _stock(x, eidx, w, mixed))
+    assert "WARNING" not in capsys.readouterr().out
+    assert pk._PF_VERDICTS == {}
+
+
+def test_a_strided_view_of_the_output_is_written_as_what_it_holds():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN)
+    dense = _launch(x, eidx, w, blobs)
+    wide = torch.full((2 * x.shape[0], x.shape[1]), 7.0, device="cuda")
+    view = wide[::2]
+    pk._prefill_launch(x, eidx, w, blobs, view)
+    torch.cuda.synchronize()
+    assert torch.equal(view, dense)
+    assert (wide[1::2] == 7.0).all()
+
+
+def test_a_strided_view_of_the_routing_weights_is_read_as_what_it_holds():
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, top_k=1, tokens=20)
+    wide = torch.zeros(w.shape[0], 3, device="cuda")
+    wide[:, 1:2] = w
+    view = wide[:, 1:2]
+    assert not view.reshape(-1).is_contiguous()
+    assert torch.equal(_launch(x, eidx, view, blobs), _launch(x, eidx, w, blobs))
+
+
+def test_fp16_activations():
+    x, eidx, w, blobs, cblobs = prefill_case(1024, 512, 4, 32, act=torch.float16,
+                                             scale_dtype=torch.float16)
+    got = _launch(x, eidx, w, blobs)
+    assert rel(got, O.stock_prefill(x, eidx, w, cblobs, act="fp16")) <= 2e-3

@@ -1,0 +1,203 @@
+// Shared device helpers for the packed-expert kernels (gfx950 / CDNA4).
+//
+// Numerics follow the reference's stock path rounding points
+// (vaayu/packed_expert_kernels.py:75-106): a packed code c becomes the weight
+//   W = round_act((c - 2^(bits-1)) * round_act(scale))
+// and every value the stock path stores in the activation dtype is rounded to it
+// (nearest-even, NaN kept NaN).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vaayu {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { DT_BF16 = 0, DT_FP16 = 1, DT_FP32 = 2 };
+
+// ── scalar loads / rounding ─────────────────────────────────────────────────────────────
+
+template <int DT>
+__device__ __forceinline__ float load_as_float(const void* p, int64_t i) {
+  if constexpr (DT == DT_BF16) {
+    uint32_t b = (uint32_t)((const uint16_t*)p)[i] << 16;
+    return __builtin_bit_cast(float, b);
+  } else if constexpr (DT == DT_FP16) {
+    return (float)((const _Float16*)p)[i];
+  } else {
+    return ((const float*)p)[i];
+  }
+}
+
+// fp32 -> the activation dtype and back: one nearest-even rounding (the hardware
+// conversions, which keep a NaN a NaN).
+template <int ACT>
+__device__ __forceinline__ float round_act(float v) {
+  if constexpr (ACT == DT_BF16) {
+    return (float)(__bf16)v;
+  } else if constexpr (ACT == DT_FP16) {
+    return (float)(_Float16)v;
+  } else {
+    return v;
+  }
+}
+
+template <int ACT>
+__device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
+  if constexpr (ACT == DT_BF16) {
+    ((__bf16*)p)[i] = (__bf16)v;
+  } else if constexpr (ACT == DT_FP16) {
+    ((_Float16*)p)[i] = (_Float16)v;
+  } else {
+    ((float*)p)[i] = v;
+  }
+}
+
+// (a & m) | o in one VALU op. gfx9 VOP3 has no literal operands, so the masks live in
+// VGPRs and the op is spelled out (the compiler otherwise emits v_and + v_or).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+  return r;
+}
+
+// SiLU(g) * u with the stock rounding points: a = round(g / (1 + exp(-g))), h = round(a*u)
+// (vaayu/packed_expert_kernels.py:147-150).
+template <int ACT>
+__device__ __forceinline__ float silu_mul(float acc_g, float acc_u) {
+  float g = round_act<ACT>(acc_g);
+  float u = round_act<ACT>(acc_u);
+  float a = round_act<ACT>(g / (1.0f + expf(-g)));
+  return round_act<ACT>(a * u);
+}
+
+// ── per-group dequant constants ─────────────────────────────────────────────────────────
+//
+// The codes are turned into fp16 values with an exponent "magic": a code c placed in the
+// low mantissa bits under exponent 2^10 reads as 1024 + c; placed at mantissa bits 4..7
+// under exponent 2^6 it reads as 64 + c. v_fma_mix then computes
+//   (1024 + c) * s - (1024 + off) * s   or   (64 + c) * s - (64 + off) * s
+// in fp32. Both addends are exact (s has <= 11 significant bits for bf16/fp16
+// activations) and the exact result (c - off) * s has <= 19 significant bits, so the one
+// fp32 rounding is exact and the later conversion to the activation dtype is the stock
+// path's single rounding of the dequantized weight.
+struct GroupK {
+  float s;       // the scale, already rounded to the activation dtype
+  float lo;      // -(1024 + off) * s
+  float hi;      // -(64 + off) * s
+};
+
+template <int BITS>
+__device__ __forceinline__ GroupK group_consts(float s_act) {
+  constexpr float off = (float)(1 << (BITS - 1));
+  GroupK k;
+  k.s = s_act;
+  k.lo = -(1024.0f + off) * s_act;
+  k.hi = -(64.0f + off) * s_act;
+  return k;
+}
+
+// ── 16-byte units: 4 words of codes -> weights in the activation dtype ─────────────────
+//
+// For bf16/fp16 activations the weights come out as packed pairs (element 2i in the low
+// half, 2i+1 in the high half), ready for v_dot2 or an MFMA operand.
+
+struct Masks {
+  uint32_t m_lo, m_hi, magic_lo, magic_hi, m_byte;
+};
+
+__device__ __forceinline__ Masks make_masks() {
+  Masks m;
+  m.m_lo = 0x000F000Fu;
+  m.m_hi = 0x00F000F0u;
+  m.magic_lo = 0x64006400u;   // fp16 2^10: mantissa bits 0..9
+  m.magic_hi = 0x54005400u;   // fp16 2^6: a code at mantissa bits 4..7 reads as 64 + c
+  m.m_byte = 0x00FF00FFu;
+  return m;
+}
+
+// int4 word (codes 0..7) -> 4 packed weight pairs in the activation dtype (bf16 or fp16).
+template <int ACT>
+__device__ __forceinline__ void deq_word_i4(uint32_t w, const GroupK& k, const Masks& M,
+                                            uint32_t out[4]) {
+  f16x2 A = __builtin_bit_cast(f16x2, and_or(w, M.m_lo, M.magic_lo));   // c0, c4
+  f16x2 B = __builtin_bit_cast(f16x2, and_or(w, M.m_hi, M.magic_hi));   // c1, c5
+  uint32_t w8 = w >> 8;
+  f16x2 C = __builtin_bit_cast(f16x2, and_or(w8, M.m_lo, M.magic_lo));  // c2, c6
+  f16x2 D = __builtin_bit_cast(f16x2, and_or(w8, M.m_hi, M.magic_hi));  // c3, c7
+  float f0 = __builtin_fmaf((float)A.x, k.s, k.lo);
+  float f1 = __builtin_fmaf((float)B.x, k.s, k.hi);
+  float f2 = __builtin_fmaf((float)C.x, k.s, k.lo);
+  float f3 = __builtin_fmaf((float)D.x, k.s, k.hi);
+  float f4 = __builtin_fmaf((float)A.y, k.s, k.lo);
+  float f5 = __builtin_fmaf((float)B.y, k.s, k.hi);
+  float f6 = __builtin_fmaf((float)C.y, k.s, k.lo);
+  float f7 = __builtin_fmaf((float)D.y, k.s, k.hi);
+  if constexpr (ACT == DT_BF16) {
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, bf16x2));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, bf16x2));
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f4, f5}, bf16x2));
+    out[3] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f6, f7}, bf16x2));
+  } else {
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, f16x2));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, f16x2));
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f4, f5}, f16x2));
+    out[3] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f6, f7}, f16x2));
+  }
+}
+
+// int8 word (codes 0..3) -> 2 packed weight pairs.
+template <int ACT>
+__device__ __forceinline__ void deq_word_i8(uint32_t w, const GroupK& k, const Masks& M,
+                                            uint32_t out[2]) {
+  f16x2 A = __builtin_bit_cast(f16x2, and_or(w, M.m_byte, M.magic_lo));       // c0, c2
+  f16x2 B = __builtin_bit_cast(f16x2, and_or(w >> 8, M.m_byte, M.magic_lo));  // c1, c3
+  float f0 = __builtin_fmaf((float)A.x, k.s, k.lo);
+  float f1 = __builtin_fmaf((float)B.x, k.s, k.lo);
+  float f2 = __builtin_fmaf((float)A.y, k.s, k.lo);
+  float f3 = __builtin_fmaf((float)B.y, k.s, k.lo);
+  if constexpr (ACT == DT_BF16) {
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, bf16x2));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, bf16x2));
+  } else {
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, f16x2));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, f16x2));
+  }
+}
+
+// Any bit width (1, 2, 4, 8) one code at a time, for any activation dtype: the general
+// path (fp32 activations and the narrow widths).
+template <int ACT, int BITS>
+__device__ __forceinline__ float deq_code(uint32_t w, int j, float s_act) {
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  float c = (float)((w >> (j * BITS)) & mask) - (float)(1 << (BITS - 1));
+  return round_act<ACT>(c * s_act);
+}
+
+// Packed-pair dot products (fp32 accumulate).
+template <int ACT>
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  if constexpr (ACT == DT_BF16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                           __builtin_bit_cast(bf16x2, x), acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, x),
+                                  acc, false);
+  }
+}
+
+// ── wavefront reductions ───────────────────────────────────────────────────────────────
+
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+}  // namespace vaayu

@@ -1,0 +1,81 @@
+// Whole-blob dequant: the packed codes of one expert (all roles, one flat stream) to dense
+// weights, bit-exact with `_fused_dequant_kernel` (vaayu/moe_patch.py:750-769):
+//   out[i] = round_out((code_i - 2^(bits-1)) * round_out(scale[i / group]))
+// The code offset is subtracted exactly in integers and the product is formed in fp32
+// (exact for bf16 / fp16 outputs; the fp32 output's own rounding for fp32), then rounded
+// once to the output dtype. Each thread handles one 16-byte unit (4 words) and writes its
+// 128/bits outputs with wide stores: a pure HBM stream.
+#include "common.hpp"
+#include "abi_internal.hpp"
+
+namespace vaayu {
+
+__device__ __forceinline__ float load_sc(const void* p, int64_t i, int dt) {
+  if (dt == DT_BF16) return load_as_float<DT_BF16>(p, i);
+  if (dt == DT_FP16) return load_as_float<DT_FP16>(p, i);
+  return load_as_float<DT_FP32>(p, i);
+}
+
+template <int BITS, int OUT>
+__global__ void __launch_bounds__(256)
+dequant_kernel(const int32_t* __restrict__ packed, const void* __restrict__ scale, int sc_dt,
+               void* __restrict__ out, int64_t n_words, int group) {
+  constexpr int PER = 32 / BITS;
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  const int64_t w0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (w0 >= n_words) return;
+  uint32_t w[4];
+  const int nw = n_words - w0 >= 4 ? 4 : (int)(n_words - w0);
+  if (nw == 4 && ((uintptr_t)(packed + w0) & 15) == 0) {
+    const uint4 v = *(const uint4*)(packed + w0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    for (int i = 0; i < 4; ++i) w[i] = i < nw ? (uint32_t)packed[w0 + i] : 0u;
+  }
+  for (int i = 0; i < nw; ++i) {
+    const int64_t e0 = (w0 + i) * PER;
+    float vals[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int64_t e = e0 + j;
+      const float s = round_act<OUT>(load_sc(scale, e / group, sc_dt));
+      const int c = (int)((w[i] >> (j * BITS)) & mask) - (1 << (BITS - 1));
+      vals[j] = round_act<OUT>((float)c * s);
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) store_act<OUT>(out, e0 + j, vals[j]);
+  }
+}
+
+}  // namespace vaayu
+
+using namespace vaayu;
+
+extern "C" int vaayu_dequant_blob(const int32_t* packed, const void* scale, int32_t scale_dtype,
+                                  void* out, int32_t out_dtype, int64_t n_words, int32_t bits,
+                                  int32_t group, void* stream) {
+  clear_error();
+  if (!packed || !scale || !out) return set_error(-1, "null pointer argument");
+  if (n_words <= 0) return set_error(-1, "n_words must be positive");
+  if (bits != 1 && bits != 2 && bits != 4 && bits != 8) return set_error(-2, "bit width");
+  if (group <= 0 || group % (32 / bits)) return set_error(-2, "group size");
+  if (scale_dtype < 0 || scale_dtype > 2 || out_dtype < 0 || out_dtype > 2)
+    return set_error(-1, "dtype code");
+  const int64_t units = (n_words + 3) / 4;
+  const dim3 grid((unsigned)((units + 255) / 256)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+#define DQ(B_, O_)                                                                         \
+  hipLaunchKernelGGL((dequant_kernel<B_, O_>), grid, block, 0, st, packed, scale, scale_dtype, \
+                     out, n_words, group)
+#define BYOUT(B_)                          \
+  if (out_dtype == DT_BF16) DQ(B_, DT_BF16); \
+  else if (out_dtype == DT_FP16) DQ(B_, DT_FP16); \
+  else DQ(B_, DT_FP32);
+  if (bits == 4) { BYOUT(4) }
+  else if (bits == 8) { BYOUT(8) }
+  else if (bits == 2) { BYOUT(2) }
+  else { BYOUT(1) }
+#undef BYOUT
+#undef DQ
+  return check_launch("dequant blob");
+}
