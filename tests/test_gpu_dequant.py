@@ -14,7 +14,15 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float16, torch.float32])
 def test_dequant_is_bit_exact(bits, gs, out_dtype, sdt):
-    (blob,) = cpu_blobs(512, 256, bits, gs, 1, scale_dtype=sdt)
+    if bits == 1:       # the repo's quantizer has no 1-bit range (qmax 0): raw codes
+        rng = np.random.default_rng(11)
+        words = rng.integers(-2 ** 31, 2 ** 31, 4096, dtype=np.int64).astype(np.int32)
+        blob = {"flat": {"packed": torch.from_numpy(words),
+                         "scale": torch.from_numpy(rng.uniform(1e-3, 1e-1, 4096 * 32 // gs)
+                                                   .astype(np.float32)).to(sdt)},
+                "geom": (1, gs, ())}
+    else:
+        (blob,) = cpu_blobs(512, 256, bits, gs, 1, scale_dtype=sdt)
     g = to_device(blob)
     got = mp._hip_dequant(g["flat"]["packed"], g["flat"]["scale"], bits, gs, out_dtype)
     want = O.dequant_flat(blob["flat"]["packed"], blob["flat"]["scale"], bits, gs, out_dtype)

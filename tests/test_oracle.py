@@ -376,3 +376,16 @@ def test_e2m1_table_and_mxfp4_upcast_known_answers():
         v = O.upcast_mxfp4(packed, np.array([[s]], np.uint8), "fp32")
         assert v[0, :4].tolist() == [0.5 * f, 1.0 * f, 6.0 * f, -6.0 * f]
     assert np.isnan(O.upcast_mxfp4(packed, np.array([[255]], np.uint8), "fp32")).all()
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 128), (8, 64)])
+def test_the_torch_quantizer_matches_the_oracle(bits, gs):
+    """vaayu_amd.synth (used to build benchmark experts in HBM) packs the same words and
+    scales as the oracle's restatement of the repo's quantizer."""
+    from vaayu_amd.synth import quantize_pack
+    w = torch.from_numpy(np.random.default_rng(bits * gs).standard_normal((32, 512)).astype(
+        np.float32) * 0.02).to(torch.bfloat16)
+    words, scale = quantize_pack(w, bits, gs, torch.float16)
+    q, s = O.quantize_symmetric(w, bits, gs)
+    assert np.array_equal(words.numpy(), O.pack_to_int32(q, bits))
+    assert torch.equal(scale, torch.from_numpy(s).to(torch.float16))
