@@ -36,10 +36,12 @@ def test_bad_arguments_are_rejected_without_a_launch():
     g = _lib.geom_struct((4, 32, (("gate", 512, 2048), ("down", 2048, 512), ("up", 512, 2048))))
     rc = lib.vaayu_decode_gate_up(None, None, None, 1, ctypes.byref(g), 0, 0, None)
     assert rc == -1 and b"null" in lib.vaayu_last_error()
+    rc = lib.vaayu_decode_gate_up(8, 256, 256, 1, ctypes.byref(g), 0, 0, None)
+    assert rc == -1 and b"aligned" in lib.vaayu_last_error()
     rc = lib.vaayu_decode_down(1, 1, 1, 2, 1, 0, ctypes.byref(g), 0, 0, 0, None)
     assert rc == -1
     bad = _lib.geom_struct((3, 32, (("gate", 512, 2048), ("down", 2048, 512), ("up", 512, 2048))))
-    rc = lib.vaayu_decode_gate_up(1, 1, 1, 1, ctypes.byref(bad), 0, 0, None)
+    rc = lib.vaayu_decode_gate_up(256, 256, 256, 1, ctypes.byref(bad), 0, 0, None)
     assert rc == -2 and b"bit width" in lib.vaayu_last_error()
     rc = lib.vaayu_prefill_gate_up(1, 1, 1, 1, 1, 1, ctypes.byref(g), 2, 0, None)
     assert rc == -2 and b"activation" in lib.vaayu_last_error()

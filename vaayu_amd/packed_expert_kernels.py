@@ -146,8 +146,9 @@ def _unsupported(geom, act_dtype, scale_dtype, w_dtype):
     unit = 128 // bits                      # codes per 16-byte unit
     if gs % unit:
         return f"group size {gs} holds less than one 16-byte unit of {bits}-bit codes"
-    if hid % unit or inter % unit:
-        return f"hidden {hid} / intermediate {inter} is not whole 16-byte units of codes"
+    if hid % (2 * unit) or inter % unit:
+        return (f"hidden {hid} / intermediate {inter} is not whole (hidden: an even number "
+                f"of) 16-byte units of codes")
     return None
 
 
