@@ -58,12 +58,21 @@ __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   }
 }
 
-// (a & m) | o in one VALU op. gfx9 VOP3 has no literal operands, so the masks live in
-// VGPRs and the op is spelled out (the compiler otherwise emits v_and + v_or).
+// A constant copied into a VGPR whose value the compiler no longer knows. gfx9 VOP3 takes
+// no literal operands, so with opaque masks `(a & m) | o` selects to one v_and_or_b32 and
+// `(m & a) | (~m & b)` to one v_bfi_b32 (the compiler otherwise splits them around the
+// literals, or turns the butterfly's selects into indexed register reads). The ops
+// themselves stay ordinary compiled code: no instruction is hand-written in inline asm,
+// so the compiler's hazard checks (e.g. the wait states a v_dot2c result needs before
+// another VALU op reads it) cover them.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// (a & m) | o; with opaque m and o one VALU op.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-  return r;
+  return (a & m) | o;
 }
 
 // SiLU(g) * u with the stock rounding points: a = round(g / (1 + exp(-g))), h = round(a*u)
@@ -113,11 +122,11 @@ struct Masks {
 
 __device__ __forceinline__ Masks make_masks() {
   Masks m;
-  m.m_lo = 0x000F000Fu;
-  m.m_hi = 0x00F000F0u;
-  m.magic_lo = 0x64006400u;   // fp16 2^10: mantissa bits 0..9
-  m.magic_hi = 0x54005400u;   // fp16 2^6: a code at mantissa bits 4..7 reads as 64 + c
-  m.m_byte = 0x00FF00FFu;
+  m.m_lo = opaque(0x000F000Fu);
+  m.m_hi = opaque(0x00F000F0u);
+  m.magic_lo = opaque(0x64006400u);   // fp16 2^10: mantissa bits 0..9
+  m.magic_hi = opaque(0x54005400u);   // fp16 2^6: a code at mantissa bits 4..7 reads as 64 + c
+  m.m_byte = opaque(0x00FF00FFu);
   return m;
 }
 

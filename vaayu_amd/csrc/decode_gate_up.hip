@@ -1,0 +1,70 @@
+// Decode gate/up entry: vaayu_decode_gate_up (kernels in decode_kernels.hpp).
+#include "decode_kernels.hpp"
+
+namespace vaayu {
+
+// Fast path: 4/8-bit codes with bf16/fp16 activations, any CH of the instantiated set.
+// General path (fp32 activations, 1/2-bit codes): CH = 1.
+template <int BITS, int ACT, int SW, int CH>
+static int gate_up_at(const void* x, const int64_t* tbl, void* h, const DecodeShape& s,
+                      const vaayu_geom* g, hipStream_t st) {
+  constexpr int XST = 4;                               // x staged: up to 4 uint4 per thread
+  const int x16 = s.units_row * Unit<BITS, ACT>::XD / 4;
+  if (x16 > 256 * XST) return set_error(-2, "decode gate/up: hidden too large to stage in LDS");
+  const int rows_per_wave = 64 / s.lpr;
+  const int64_t waves = (int64_t)s.n_pairs * ((s.inter + rows_per_wave - 1) / rows_per_wave);
+  hipLaunchKernelGGL((decode_gate_up_kernel<BITS, ACT, SW, 1, CH, XST>),
+                     dim3((unsigned)((waves + 3) / 4)), dim3(256), (size_t)x16 * 16, st,
+                     (const uint32_t*)x, tbl, h, s, (uint32_t)(g->gate_w * 4),
+                     (uint32_t)g->gate_s, (uint32_t)(g->up_w * 4), (uint32_t)g->up_s);
+  return 0;
+}
+
+template <int BITS, int ACT, int SW>
+static int by_ch(const void* x, const int64_t* tbl, void* h, const DecodeShape& s,
+                 const vaayu_geom* g, hipStream_t st) {
+  constexpr bool fast = Unit<BITS, ACT>::FAST;
+  switch (s.chunks) {
+    case 1: return gate_up_at<BITS, ACT, SW, 1>(x, tbl, h, s, g, st);
+    case 2: if constexpr (fast) return gate_up_at<BITS, ACT, SW, 2>(x, tbl, h, s, g, st); break;
+    case 3: if constexpr (fast) return gate_up_at<BITS, ACT, SW, 3>(x, tbl, h, s, g, st); break;
+    case 4: if constexpr (fast) return gate_up_at<BITS, ACT, SW, 4>(x, tbl, h, s, g, st); break;
+    case 7: if constexpr (fast) return gate_up_at<BITS, ACT, SW, 7>(x, tbl, h, s, g, st); break;
+  }
+  return set_error(-2, "decode gate/up: no kernel for this row split");
+}
+
+template <int BITS, int ACT>
+static int by_sw(const void* x, const int64_t* tbl, void* h, const DecodeShape& s,
+                 const vaayu_geom* g, int sc, hipStream_t st) {
+  if (sc == DT_FP32) return by_ch<BITS, ACT, 32>(x, tbl, h, s, g, st);
+  return by_ch<BITS, ACT, 16>(x, tbl, h, s, g, st);
+}
+
+}  // namespace vaayu
+
+using namespace vaayu;
+
+extern "C" int vaayu_decode_gate_up(const void* x, const int64_t* table, void* h, int32_t n_pairs,
+                                    const vaayu_geom* geom, int32_t act, int32_t scale_dtype,
+                                    void* stream) {
+  clear_error();
+  if (!x || !table || !h || !geom) return set_error(-1, "null pointer argument");
+  if (n_pairs <= 0) return set_error(-1, "n_pairs must be positive");
+  if (scale_dtype < 0 || scale_dtype > 2) return set_error(-1, "scale dtype");
+  if (((uintptr_t)x) & 15) return set_error(-1, "x must be 16-byte aligned");
+  if (const char* why = decode_unsupported(geom, act)) return set_error(-2, why);
+  const bool fast = (geom->bits == 4 || geom->bits == 8) && act != DT_FP32;
+  const Plan pl = plan_row(geom->hidden * geom->bits / 128, 2, 2, fast);
+  if (pl.lpr == 0) return set_error(-2, "decode gate/up: no lane split of this row is built");
+  const DecodeShape s = shape_for(geom, n_pairs, geom->hidden, geom->inter, scale_dtype, pl);
+  hipStream_t st = (hipStream_t)stream;
+  int rc;
+#define BA(B_, A_) else if (geom->bits == B_ && act == A_) rc = by_sw<B_, A_>(x, table, h, s, geom, scale_dtype, st);
+  if (false) rc = 0;
+  BA(4, 0) BA(4, 1) BA(4, 2) BA(8, 0) BA(8, 1) BA(8, 2) BA(2, 0) BA(2, 1) BA(2, 2)
+  BA(1, 0) BA(1, 1) BA(1, 2)
+  else rc = set_error(-2, "unsupported bit width / activation dtype");
+#undef BA
+  return rc ? rc : check_launch("decode gate/up");
+}
