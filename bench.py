@@ -39,7 +39,88 @@ def parse():
                    help="distinct random layers; the rest are byte copies at new addresses")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--summarize", nargs="+", metavar="DIR",
+                   help="print a text summary of rocprofv3 csv output directories "
+                        "(a --kernel-trace --stats run and --pmc FETCH_SIZE / WRITE_SIZE runs) "
+                        "and exit; no GPU is used")
     return p.parse_args()
+
+
+# ── rocprofv3 summaries ─────────────────────────────────────────────────────────────────
+#
+# Every run does one calibration pass first: an elementwise negation of a 256 MiB fp32
+# buffer into another (reads exactly 256 MiB, writes exactly 256 MiB). FETCH_SIZE and
+# WRITE_SIZE of a dispatch are scaled by (256 MiB / what the counter reads for that
+# calibration dispatch), which turns the counters into HBM bytes.
+CALIB_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_qwen3_b1_traffic.txt")
+
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        with open(f, newline="") as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def _short(name):
+    name = name.split("(")[0]
+    return name[:90]
+
+
+def summarize(dirs):
+    """Text summary of rocprofv3 csv output: per-kernel durations (kernel_stats.csv) and
+    per-kernel average FETCH_SIZE / WRITE_SIZE (counter_collection.csv), scaled by the
+    calibration dispatch."""
+    out = []
+    for d in dirs:
+        for r in _csv_rows(d, "kernel_stats.csv"):
+            if not out:
+                out.append(f"{'kernel':<90} {'calls':>7} {'avg us':>9} {'min us':>9} "
+                           f"{'max us':>9} {'%':>6}")
+            out.append(f"{_short(r['Name']):<90} {int(r['Calls']):>7} "
+                       f"{float(r['AverageNs']) / 1e3:>9.3f} {float(r['MinNs']) / 1e3:>9.3f} "
+                       f"{float(r['MaxNs']) / 1e3:>9.3f} {float(r['Percentage']):>6.2f}")
+    per = {}
+    for d in dirs:
+        for r in _csv_rows(d, "counter_collection.csv"):
+            key = (_short(r["Kernel_Name"]), r["Counter_Name"])
+            per.setdefault(key, []).append(float(r["Counter_Value"]))
+    if per:
+        factors = {}
+        for (name, ctr), vals in per.items():
+            if "neg" in name:       # the calibration dispatch: 256 MiB each way
+                factors[ctr] = CALIB_BYTES / (max(vals) * 1024.0)
+        out.append("")
+        out.append("counter scale factors (HBM bytes per KiB counted, from the calibration "
+                   "copy of 256 MiB): " + ", ".join(f"{c} {f * 1024:.4f}"
+                                                     for c, f in sorted(factors.items())))
+        out.append(f"{'kernel':<90} {'counter':>10} {'dispatches':>10} {'avg KiB':>12} "
+                   f"{'bytes/launch':>14}")
+        for (name, ctr), vals in sorted(per.items()):
+            avg = sum(vals) / len(vals)
+            scaled = avg * 1024.0 * factors.get(ctr, 1.0)
+            out.append(f"{name:<90} {ctr:>10} {len(vals):>10} {avg:>12.1f} {scaled:>14.0f}")
+            if "decode_gate_up_kernel" in name:
+                out.append(f"traffic_bytes decode_gate_up_kernel {ctr} {scaled:.0f}")
+    return "\n".join(out)
+
+
+def traffic_from_profile():
+    """HBM bytes per gate/up launch (FETCH_SIZE + WRITE_SIZE, scaled) from the committed
+    counter summary of this workload, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    total, seen = 0.0, set()
+    for line in open(TRAFFIC_FILE):
+        f = line.split()
+        if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == "decode_gate_up_kernel":
+            total += float(f[3])
+            seen.add(f[2])
+    return round(total) if seen == {"FETCH_SIZE", "WRITE_SIZE"} else None
 
 
 def log(msg):
@@ -54,6 +135,9 @@ def route(logits, top_k):
 
 def main():
     args = parse()
+    if args.summarize:
+        print(summarize(args.summarize))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -123,6 +207,14 @@ def main():
 
     def check(rc):
         _lib.check(rc, "bench launch")
+
+    # counter calibration: a plain elementwise pass of known size (256 MiB read, 256 MiB
+    # written), so profiles of this run can scale FETCH_SIZE / WRITE_SIZE to bytes
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
 
     # eager once (validates every launch), then graphs
     st = torch.cuda.current_stream().cuda_stream
@@ -211,7 +303,7 @@ def main():
         "layer_hbm_gbs": round(layer_gbs, 1),
         "roofline": {"bound": "hbm", "kernel": "decode_gate_up_kernel",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
                      "bytes_per_launch": gu_bytes,
                      "us_per_launch": round(ms_gu * 1000 / L, 3)},
         "down_kernel": {"achieved_gbs": round(dn_gbs, 1), "bytes_per_launch": dn_bytes,
