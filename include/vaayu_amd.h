@@ -92,6 +92,27 @@ int vaayu_dequant_blob(const int32_t *packed, const void *scale, int32_t scale_d
                        int32_t out_dtype, int64_t n_words, int32_t bits, int32_t group,
                        void *stream);
 
+/* FP8 e4m3 block-scaled dequant. Replaces `dequantize_block_scaled`
+ * (vaayu/model_code/deepseek_v4/modeling_deepseek_v4.py:228-240):
+ * out[i, j] = round_out(fp32(weight[i, j]) * fp32(scale[i / bo, j / bi])), the fp32 product
+ * rounded once, with bo = rows / scale_rows and bi = cols / scale_cols derived from the shapes.
+ * weight uint8 [rows, cols] (float8_e4m3fn bits), row-major; scale [scale_rows, scale_cols] of
+ * scale_dtype 0 bf16, 1 fp16, 2 fp32, 3 e8m0 (uint8 exponent, 0xFF = NaN); out [rows, cols]
+ * of out_dtype 0 bf16, 1 fp16, 2 fp32. cols and bi multiples of 16. Bit-exact. */
+int vaayu_dequant_fp8_block(const uint8_t *weight, const void *scale, int32_t scale_dtype,
+                            void *out, int32_t out_dtype, int64_t rows, int64_t cols,
+                            int64_t scale_rows, int64_t scale_cols, void *stream);
+
+/* Microscaled upcast along the last axis. Replaces `upcast_from_mxfp_torch` and its Triton
+ * twin `_upcast_from_mxfp` (vendor gpt_oss_triton_kernels numerics_details/mxfp.py:256-299,
+ * mxfp_details/_upcast_from_mxfp.py:8-122): out[r, e] = round_out(fp32(q[r, e]) * 2^(s - 127))
+ * with s = scale[r, e / 32] taken as the fp32 of exponent bits s (s = 0 gives 0) and
+ * s = 0xFF giving NaN. fmt 0: e2m1, two per byte, even element in the low nibble
+ * (q [rows, k / 2]); fmt 1: e4m3 (q [rows, k]). scale uint8 [rows, ceil(k / 32)]; out
+ * [rows, k] of out_dtype 0 bf16, 1 fp16, 2 fp32. Bit-exact. */
+int vaayu_upcast_mx(const uint8_t *q, int32_t fmt, const uint8_t *scale, void *out,
+                    int32_t out_dtype, int64_t rows, int64_t k, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

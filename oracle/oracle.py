@@ -490,6 +490,18 @@ def upcast_mxfp4(packed_u8, scale_e8m0, act="bf16") -> np.ndarray:
     return round_to((vals * full).astype(np.float32), act_name(act))
 
 
+def upcast_mx_e4m3(codes_u8, scale_e8m0, act="bf16") -> np.ndarray:
+    """`upcast_from_mxfp_torch` for float8_e4m3fn codes (vendor …/numerics_details/mxfp.py:
+    276-279: `tensor.to(float32)`), otherwise as `upcast_mxfp4`: 2^(s-127) per 32 elements
+    along the last axis, fp32 product, one cast; scale 0xFF is NaN."""
+    vals = e4m3_value(codes_u8)
+    s = np.asarray(scale_e8m0, dtype=np.uint8).astype(np.uint32)
+    sf = (s << np.uint32(23)).view(np.float32)
+    sf = np.where(s == 0xFF, np.float32(np.nan), sf)
+    full = np.repeat(sf, 32, axis=-1)[..., :vals.shape[-1]]
+    return round_to((vals * full).astype(np.float32), act_name(act))
+
+
 # ── the CPU baseline: the stock loop itself on torch CPU ─────────────────────────────────
 
 def _dequant_torch(blob, dtype):

@@ -376,6 +376,18 @@ def test_e2m1_table_and_mxfp4_upcast_known_answers():
         v = O.upcast_mxfp4(packed, np.array([[s]], np.uint8), "fp32")
         assert v[0, :4].tolist() == [0.5 * f, 1.0 * f, 6.0 * f, -6.0 * f]
     assert np.isnan(O.upcast_mxfp4(packed, np.array([[255]], np.uint8), "fp32")).all()
+    assert not O.upcast_mxfp4(packed, np.array([[0]], np.uint8), "fp32").any()   # s << 23 = 0.0
+
+
+def test_mx_e4m3_upcast_known_answers():
+    codes = np.zeros((1, 32), np.uint8)
+    codes[0, :5] = [0x38, 0x40, 0x01, 0xB8, 0x7F]        # 1, 2, 2^-9, -1, NaN
+    v = O.upcast_mx_e4m3(codes, np.array([[130]], np.uint8), "fp32")   # x 8
+    assert v[0, :4].tolist() == [8.0, 16.0, 2.0 ** -6, -8.0] and np.isnan(v[0, 4])
+    assert np.isnan(O.upcast_mx_e4m3(codes, np.array([[255]], np.uint8), "fp32")).all()
+    # a bf16 cast that rounds: 1.125 * 2^0 in e4m3 (0x39) is exact in bf16; 0x3F = 1.875
+    codes[0, :2] = [0x39, 0x3F]
+    assert O.upcast_mx_e4m3(codes, np.array([[127]], np.uint8), "bf16")[0, :2].tolist() == [1.125, 1.875]
 
 
 @pytest.mark.parametrize("bits,gs", [(4, 32), (4, 128), (8, 64)])

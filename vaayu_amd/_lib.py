@@ -17,7 +17,7 @@ DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 EXPORTS = ("vaayu_abi_version", "vaayu_last_error", "vaayu_decode_gate_up", "vaayu_decode_down",
            "vaayu_prefill_gate_up", "vaayu_prefill_down", "vaayu_prefill_reduce",
-           "vaayu_dequant_blob")
+           "vaayu_dequant_blob", "vaayu_dequant_fp8_block", "vaayu_upcast_mx")
 
 
 class Geom(ctypes.Structure):
@@ -50,6 +50,8 @@ def _bind(lib):
                                [vp, vp, vp, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
         "vaayu_prefill_reduce": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp]),
         "vaayu_dequant_blob": (ctypes.c_int, [vp, vp, i32, vp, i32, i64, i32, i32, vp]),
+        "vaayu_dequant_fp8_block": (ctypes.c_int, [vp, vp, i32, vp, i32, i64, i64, i64, i64, vp]),
+        "vaayu_upcast_mx": (ctypes.c_int, [vp, i32, vp, vp, i32, i64, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
