@@ -39,6 +39,9 @@ def parse():
                    help="distinct random layers; the rest are byte copies at new addresses")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--workload", default="qwen3-decode", choices=sorted(WORKLOADS),
+                   help="qwen3-decode (default) is the headline line; the others are the "
+                        "prefill-path shapes")
     p.add_argument("--summarize", nargs="+", metavar="DIR",
                    help="print a text summary of rocprofv3 csv output directories "
                         "(a --kernel-trace --stats run and --pmc FETCH_SIZE / WRITE_SIZE runs) "
@@ -133,6 +136,203 @@ def route(logits, top_k):
     return w / w.sum(dim=-1, keepdim=True), idx
 
 
+# ── prefill-path workloads ──────────────────────────────────────────────────────────────
+#
+# A multi-token call runs the three grouped kernels (gate/up, down, the expert-id-order
+# reduce) over the call's tables. The tables and activations are resident before timing
+# (the engine builds them from the call's routing on the host); the three launches are
+# recorded in one HIP graph and replayed.
+WORKLOADS = {
+    "qwen3-decode": None,      # the headline decode line (main)
+    "dsv3-prefill": dict(name="DeepSeek-V3-shape MoE layer prefill, 2048 tokens", hidden=7168,
+                         inter=2048, experts=256, top_k=8, tokens=2048, routing="zipf",
+                         shared=True, bound="mfma"),
+    "mixtral-prefill": dict(name="Mixtral-8x7B-shape MoE layer prefill, 512 tokens", hidden=4096,
+                            inter=14336, experts=8, top_k=2, tokens=512, routing="softmax",
+                            shared=False, bound="mfma"),
+    "qwen3-decode-b8": dict(name="Qwen3-30B-A3B-shape MoE layer decode, batch of 8 tokens",
+                            hidden=2048, inter=768, experts=128, top_k=8, tokens=8,
+                            routing="softmax", shared=False, bound="hbm"),
+}
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def zipf_routing(tokens, experts, top_k, s, gen):
+    """top_k distinct experts per token drawn with probability proportional to
+    1 / rank^s over a random ranking of the experts; weights softmax(random logits) of
+    the chosen, renormalised."""
+    rank = torch.randperm(experts, generator=gen)
+    p = 1.0 / (rank.double() + 1.0) ** s
+    idx = torch.multinomial(p.expand(tokens, experts), top_k, replacement=False, generator=gen)
+    w = torch.randn(tokens, top_k, generator=gen).softmax(-1)
+    return w, idx
+
+
+def bench_prefill(args, spec):
+    import vaayu_amd.packed_expert_kernels as pk
+    from vaayu_amd.synth import random_expert
+    from oracle import oracle as O
+
+    if pk.triton is None:
+        raise SystemExit("vaayu_amd kernel library missing: run `python -m vaayu_amd.build`")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, I, E, K, T = spec["hidden"], spec["inter"], spec["experts"], spec["top_k"], spec["tokens"]
+    BITS, GS = 4, 128
+    t0 = time.time()
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    n_exp = E + (1 if spec["shared"] else 0)
+    blobs = {e: random_expert(H, I, BITS, GS, generator=gen, device=dev, std=0.02,
+                              scale_dtype=torch.float16) for e in range(n_exp)}
+    torch.cuda.synchronize()
+    per_expert = sum(t.numel() * t.element_size() for t in blobs[0]["flat"].values())
+    log(f"{n_exp} experts resident: {n_exp * per_expert / 1e9:.2f} GB ({time.time() - t0:.1f} s)")
+    cg = torch.Generator().manual_seed(99)
+    x = torch.randn(T, H, generator=cg).to(torch.bfloat16).to(dev)
+    if spec["routing"] == "zipf":
+        w, eidx = zipf_routing(T, E, K, 1.1, cg)
+    else:
+        w, eidx = route(torch.randn(T, E, generator=cg), K)
+    w = w.to(dev)
+    geom = blobs[0]["geom"]
+    sc = pk._DTYPE_CODE[torch.float16]
+
+    # calls of this layer: the routed experts, then (DeepSeek) the shared expert as a
+    # one-slot call over every token with weight 1, added after the routed sum is cast
+    calls = [(eidx, w, K)]
+    if spec["shared"]:
+        calls.append((torch.full((T, 1), E, dtype=torch.int64), torch.ones(T, 1, device=dev), 1))
+    prepared = []
+    for ei, wi, k in calls:
+        plan = pk._prefill_plan(ei)
+        tbl, rows, order, n_blocks = pk._prefill_tables(ei, plan, blobs, dev)
+        tbl, rows, order = tbl.clone(), rows.clone(), order.clone()     # off the table ring
+        h = torch.empty(T * k, I, dtype=torch.bfloat16, device=dev)
+        y = torch.empty(T * k, H, dtype=torch.float32, device=dev)
+        out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        prepared.append((tbl, rows, order, n_blocks, k, wi, h, y, out, int(plan[1].numel())))
+    torch.cuda.synchronize()
+
+    def run_layer():
+        for tbl, rows, order, n_blocks, k, wi, h, y, out, _live in prepared:
+            pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h)
+            pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y)
+            pk._reduce(y, order, out, k)
+
+    def run_stage(stage):
+        for tbl, rows, order, n_blocks, k, wi, h, y, out, _live in prepared:
+            if stage == "gate_up":
+                pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h)
+            elif stage == "down":
+                pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y)
+            else:
+                pk._reduce(y, order, out, k)
+
+    run_layer()
+    torch.cuda.synchronize()
+
+    def capture(fn):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph
+
+    def time_graph(graph, steps, warmup):
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+
+    steps = max(1, args.steps // (5 if T >= 512 else 1))
+    stage_ms = {st: time_graph(capture(lambda st=st: run_stage(st)), steps, args.warmup)
+                for st in ("gate_up", "down", "reduce")}
+    ms = time_graph(capture(run_layer), steps, args.warmup)
+    flops = 2 * T * K * 3 * H * I + (2 * T * 3 * H * I if spec["shared"] else 0)
+    live = sum(p[-1] for p in prepared)
+    wbytes = live * per_expert
+    act_bytes = sum(T * H * 2 + 2 * T * k * I * 2 + T * k * H * 4 * 2 + T * H * 4
+                    for *_r, k, _wi, _h, _y, _o, _l in prepared)
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
+    log(f"layer {ms * 1000:.1f} us = {ms * 1000 / T:.3f} us/token; {tflops:.1f} TFLOP/s "
+        f"({tflops / MFMA_PEAK_TFLOPS:.1%} of bf16 MFMA peak), {gbs:.0f} GB/s; stages "
+        + ", ".join(f"{k} {v * 1000:.1f} us" for k, v in stage_ms.items()))
+
+    # parity: a few tokens against the oracle (each token's output depends on its own
+    # routing only)
+    outs = [p[8] for p in prepared]
+    n_chk = 2 if H * I > 4e6 else 8
+    tok = torch.randperm(T, generator=cg)[:n_chk].tolist()
+    cpu_blob = {}
+
+    def cblob(e):
+        if e not in cpu_blob:
+            cpu_blob[e] = {"flat": {n: t.cpu() for n, t in blobs[e]["flat"].items()}, "geom": geom}
+        return cpu_blob[e]
+
+    worst = {"relL2": 0.0, "max_abs": 0.0}
+    for t in tok:
+        for (ei, wi, k), out in zip(calls, outs):
+            ids = ei[t].tolist()
+            order = sorted(range(k), key=lambda s: ids[s])
+            ref = O.stock_decode(x[t:t + 1].cpu(), [(cblob(ids[s]), s) for s in order],
+                                 wi[t].cpu())
+            got = out[t:t + 1].cpu().numpy()
+            worst["relL2"] = max(worst["relL2"], O.rel_l2(got, ref))
+            worst["max_abs"] = max(worst["max_abs"], float(np.abs(got - ref).max()))
+    parity = dict(worst, tokens_checked=n_chk, tolerance={"relL2": 5e-3, "max_abs": 2e-2})
+    log(f"parity vs oracle on {n_chk} tokens: {parity}")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+        sub = 2 if H * I > 4e6 else 8
+        ei, wi, k = calls[0]
+        cb = {e: cblob(e) for e in set(ei[:sub].reshape(-1).tolist())}
+        o = torch.empty(sub, H)
+        n_calls, t_start = 0, time.perf_counter()
+        while time.perf_counter() - t_start < args.cpu_seconds or n_calls == 0:
+            O.stock_prefill_torch(x[:sub].cpu(), ei[:sub], wi[:sub].cpu(), cb, o)
+            n_calls += 1
+        cpu_s = time.perf_counter() - t_start
+        cpu = {"value": cpu_s * 1e6 / (n_calls * sub), "unit": "us/token per MoE layer",
+               "cores": threads, "kind": "port",
+               "sample": f"{n_calls} stock prefill calls of {sub} tokens of this layer's routed "
+                         f"experts on torch CPU (bf16 weights dequantized per call, fp32 GEMMs), "
+                         f"{cpu_s:.1f} s"}
+        log(f"cpu baseline {cpu}")
+
+    bound = spec["bound"]
+    roof = ({"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
+             "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4)}
+            if bound == "mfma" else
+            {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    roof.update({"traffic": None, "kernels": "prefill_gate_up + prefill_down + prefill_reduce",
+                 "flops_per_call": flops, "bytes_per_call": wbytes + act_bytes})
+    result = {
+        "metric": METRIC, "value": round(ms * 1000 / T, 4), "unit": "us/token",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": spec["name"] + ", int4 g128 fp16 scales", "hidden": H,
+                   "experts": E, "inter": I, "top_k": K, "tokens": T,
+                   "shared_expert": spec["shared"], "routing": spec["routing"],
+                   "parallelism": "none (one GPU)"},
+        "tokens_per_s_per_layer": round(T / (ms * 1e-3), 1),
+        "stage_us": {k: round(v * 1000, 2) for k, v in stage_ms.items()},
+        "roofline": roof, "parity": parity, "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize:
@@ -144,6 +344,9 @@ def main():
               "(expert-parallel sharding is a design note only). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload != "qwen3-decode":
+        bench_prefill(args, WORKLOADS[args.workload])
+        return
 
     import vaayu_amd.packed_expert_kernels as pk
     from vaayu_amd import _lib
