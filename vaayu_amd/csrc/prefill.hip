@@ -63,55 +63,80 @@ __device__ __forceinline__ void unit_operands(uint4 q, float s_act, const Masks&
 
 // ── run-tiled grouped GEMM ─────────────────────────────────────────────────────────────
 //
-// A work item is a RUN of up to kRun consecutive 16-row blocks of one expert (the table
-// lists each expert's blocks contiguously) times 64 weight rows (N). Runs split where the
-// expert changes and at block indices that are multiples of kRun, so a block can tell from
-// the table alone whether it leads a run (its predecessor is another expert, or its index
-// is a multiple of kRun) and how long the run is; items of non-leading blocks exit at once.
+// A work item is a RUN of up to R consecutive 16-row blocks of one expert (the table lists
+// each expert's blocks contiguously) times kTileN weight rows (N); R is kRunGateUp for gate/up,
+// whose two roles hold twice the accumulators, and kRunDown for down. Runs split where the
+// expert changes and at block indices that are multiples of R, so a block can tell from the
+// table alone whether it leads a run (its predecessor is another expert, or its index is a
+// multiple of R) and how long the run is; items of non-leading blocks exit at once. The
+// kernels branch once on the run's length S to a K loop compiled for that S.
 //
 // Per K step (4 units of codes per weight row) the block stages the run's activation rows
-// for that step in LDS (prefetched one step ahead in registers), each wave dequantizes its
-// 16 weight rows' codes ONCE in VGPRs straight into MFMA B operands and runs them against
-// every 16-row sub-tile of the run: the dequant cost is shared by up to kRun*16 rows. The
-// A operand of sub-tile s comes from LDS with the same K-slot map as B (quarter q of the
-// wave, MFMA i: codes [q*CPU + 8i, +8) of the step).
+// in LDS, each wave dequantizes its 16 weight rows' codes ONCE in VGPRs straight into MFMA B
+// operands and runs them against every 16-row sub-tile of the run: the dequant cost is
+// shared by up to R*16 rows. The A operand of sub-tile s comes from LDS with the same K-slot
+// map as B (quarter q of the wave, MFMA i: codes [q*CPU + 8i, +8) of the step).
 //
-// XCD mapping: linear workgroup id L runs on XCD L % 8. Blocks are grouped by b / kRun
-// (at most one full run per group) and group G is placed on XCD G % 8, with all of a
-// group's N tiles consecutive in that XCD's order, so the items that share a run's
-// activation rows share an L2.
-constexpr int kRun = 8;
-constexpr int kStride = 16;      // LDS row padding, bytes
+// XCD mapping: linear workgroup id L runs on XCD L % 8. Blocks are grouped by b / R (at most
+// one full run per group) and group G is placed on XCD G % 8, with all of a group's N tiles
+// consecutive in that XCD's order, so the items that share a run's activation rows share an
+// L2.
+
+// MFMA B operand i (8 weights as 4 packed pairs) of one unit of codes: word i (4-bit
+// codes) or words 2i, 2i+1 (8-bit codes).
+template <int BITS, int ACT>
+__device__ __forceinline__ void operand_of(uint4 q, float s_act, const Masks& M, int i, uint4& b) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (BITS == 4) {
+    uint32_t p[4];
+    deq_word_i4<ACT>(w[i], group_consts<4>(s_act), M, p);
+    b = make_uint4(p[0], p[1], p[2], p[3]);
+  } else {
+    const GroupK k = group_consts<8>(s_act);
+    uint32_t p0[2], p1[2];
+    deq_word_i8<ACT>(w[2 * i], k, M, p0);
+    deq_word_i8<ACT>(w[2 * i + 1], k, M, p1);
+    b = make_uint4(p0[0], p0[1], p1[0], p1[1]);
+  }
+}
+
+constexpr int kRunGateUp = 8;    // blocks per run, gate/up (two roles of accumulators)
+constexpr int kRunDown = 8;      // blocks per run, down
+constexpr int kWaves = 8;        // waves per workgroup, 16 weight rows (N) each
+constexpr int kTileN = 16 * kWaves;
 
 struct RunInfo {
   int lead;       // 1 if this item computes
   int nblk;       // blocks in the run
 };
 
+template <int R>
 __device__ __forceinline__ RunInfo run_of(const int64_t* __restrict__ tbl, int b, int n_blocks) {
   RunInfo r{0, 0};
   if (b >= n_blocks) return r;
   const int64_t me = tbl[2 * b];
-  if (b % kRun != 0 && tbl[2 * (b - 1)] == me) return r;
+  if (b % R != 0 && tbl[2 * (b - 1)] == me) return r;
   int n = 1;
-  while (n < kRun && b + n < n_blocks && (b + n) % kRun != 0 && tbl[2 * (b + n)] == me) ++n;
+  while (n < R && b + n < n_blocks && (b + n) % R != 0 && tbl[2 * (b + n)] == me) ++n;
   r.lead = 1;
   r.nblk = n;
   return r;
 }
 
 // (block b, N tile) of linear workgroup id L.
+template <int R>
 __device__ __forceinline__ void item_of(int L, int n_tiles, int& b, int& tile) {
   const int xcd = L & 7, j = L >> 3;
-  const int per_group = kRun * n_tiles;                  // items of one group of blocks
+  const int per_group = R * n_tiles;                     // items of one group of blocks
   const int g = j / per_group, w = j - g * per_group;
-  b = (g * 8 + xcd) * kRun + w / n_tiles;
+  b = (g * 8 + xcd) * R + w / n_tiles;
   tile = w % n_tiles;
 }
 
+template <int R>
 __host__ __device__ inline int items_for(int n_blocks, int n_tiles) {
-  const int groups = (n_blocks + kRun - 1) / kRun;
-  return ((groups + 7) / 8) * 8 * kRun * n_tiles;
+  const int groups = (n_blocks + R - 1) / R;
+  return ((groups + 7) / 8) * 8 * R * n_tiles;
 }
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -130,54 +155,64 @@ __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
 // K offset added to it.
 constexpr uint32_t kNoRow = 0xFFFF0000u;
 
-// One K step of the run's activation rows: S*16 rows x KS codes (KS*2 bytes a row), in
-// 16-byte pieces; piece t of thread i is row (t*256 + i) / PPR, piece (t*256 + i) % PPR.
-// off[t] is that piece's byte offset in the activation buffer at K = 0 (kNoRow: padding).
-template <int KS>
+// One K step of a run's activation rows (S*16 rows x KS codes, RB = KS*2 bytes a row) lives
+// in LDS as S*16 rows of RB bytes, row r's 16-byte piece c at position c ^ (r % PPR): the
+// A reads of one MFMA (16 rows at one piece) then fall on distinct banks. Rows reach LDS by
+// direct buffer->LDS loads: one wave instruction writes 1 KB (64 lanes x 16 B) contiguously,
+// i.e. 1024/RB rows, so lane l of instruction g loads row g*(1024/RB) + l/PPR, the piece
+// that belongs at position l % PPR. off[j] is lane's byte offset (at K = 0) in the
+// activation buffer for its j-th instruction g = kWaves*j + wave (kNoRow: a padding row, read as
+// zeros by the bounds check).
+template <int KS, int S>
 struct AStage {
-  static constexpr int PPR = KS * 2 / 16;               // 16-byte pieces per row
-  static constexpr int PER = kRun * 16 * PPR / 256;     // pieces per thread (full run)
-  static constexpr int ROWS_PER_T = 256 / PPR;          // rows one piece index t covers
+  static constexpr int RB = KS * 2;                     // bytes per staged row
+  static constexpr int PPR = RB / 16;                   // 16-byte pieces per row
+  static constexpr int RPI = 1024 / RB;                 // rows per wave instruction
+  static constexpr int INSTR = S * 16 / RPI;            // instructions per step (block)
+  static constexpr int PER = (INSTR + kWaves - 1) / kWaves;   // per wave
+  static constexpr int BYTES = S * 16 * RB;             // one step's rows
   uint32_t off[PER];
-  uint4 v[PER];
 };
 
-// Piece offsets of this thread; `row_off(r)` = byte offset of run row r (kNoRow: padding).
-template <int KS, typename RowOff>
-__device__ __forceinline__ void a_plan(AStage<KS>& a, int S, RowOff row_off) {
-  constexpr int PPR = AStage<KS>::PPR;
+template <int KS, int S, typename RowOff>
+__device__ __forceinline__ void a_plan(AStage<KS, S>& a, RowOff row_off) {
+  using A = AStage<KS, S>;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < AStage<KS>::PER; ++t) {
-    const int idx = t * 256 + (int)threadIdx.x;
-    const int r = idx / PPR, c = idx % PPR;
-    const uint32_t ro = r < S * 16 ? row_off(r) : kNoRow;
-    a.off[t] = ro == kNoRow ? kNoRow : ro + c * 16;
+  for (int j = 0; j < A::PER; ++j) {
+    const int g = kWaves * j + w;
+    const int r = g * A::RPI + l / A::PPR;
+    const int c = (l % A::PPR) ^ (r % A::PPR);
+    const uint32_t ro = g < A::INSTR ? row_off(r) : kNoRow;
+    a.off[j] = ro == kNoRow ? kNoRow : ro + c * 16;
   }
 }
 
-template <int KS>
-__device__ __forceinline__ bool a_live(int t, int S) {   // block-uniform
-  return t * AStage<KS>::ROWS_PER_T < S * 16;
-}
-
-template <int KS>
-__device__ __forceinline__ void a_load(AStage<KS>& a, rsrc_t src, int S, int k0) {
+// Issue one step's rows into `buf` (wave-uniform LDS address of the step's tile).
+template <int KS, int S>
+__device__ __forceinline__ void a_issue(const AStage<KS, S>& a, rsrc_t src, char* buf, int k0) {
+  using A = AStage<KS, S>;
+  const int w = threadIdx.x >> 6;
 #pragma unroll
-  for (int t = 0; t < AStage<KS>::PER; ++t)
-    if (a_live<KS>(t, S)) a.v[t] = bload16(src, a.off[t] + (uint32_t)k0 * 2u);
-}
-
-template <int KS>
-__device__ __forceinline__ void a_store(const AStage<KS>& a, char* lds, int S) {
-  constexpr int PPR = AStage<KS>::PPR;
-  constexpr int LROW = KS * 2 + kStride;
-#pragma unroll
-  for (int t = 0; t < AStage<KS>::PER; ++t) {
-    if (a_live<KS>(t, S)) {
-      const int idx = t * 256 + (int)threadIdx.x;
-      *(uint4*)(lds + (idx / PPR) * LROW + (idx % PPR) * 16) = a.v[t];
+  for (int j = 0; j < A::PER; ++j) {
+    const int g = kWaves * j + w;
+    if (A::INSTR % kWaves == 0 || g < A::INSTR) {
+#if defined(__HIP_DEVICE_COMPILE__)        // a gfx950 instruction: no host-pass form
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          src, (__attribute__((address_space(3))) void*)(buf + g * 1024), 16,
+          a.off[j] + (uint32_t)k0 * 2u, 0, 0, 0);
+#endif
     }
   }
+}
+
+// The A operand of MFMA (s, i) for lane (q, m): row 16s + m, piece q*CPU/8 + i.
+template <int KS, int S, int CPU>
+__device__ __forceinline__ uint4 a_read(const char* buf, int s, int i, int q, int m) {
+  using A = AStage<KS, S>;
+  const int r = s * 16 + m;
+  const int piece = q * (CPU / 8) + i;
+  return *(const uint4*)(buf + r * A::RB + ((piece ^ (r % A::PPR)) * 16));
 }
 
 // B codes and raw scale bits of one K step for one weight row (lane q's unit).
@@ -186,187 +221,267 @@ struct BStep {
   uint32_t s;
 };
 
-// Scale bits of dtype dt (wave-uniform) as fp32.
-__device__ __forceinline__ float scale_of(uint32_t b, int dt) {
-  if (dt == DT_FP32) return __builtin_bit_cast(float, b);
-  const float bf = __builtin_bit_cast(float, b << 16);
-  const float hf = (float)__builtin_bit_cast(_Float16, (uint16_t)b);
-  return dt == DT_BF16 ? bf : hf;
+// Raw scale bits as fp32. SW = 32: fp32 bits. SW = 16: bf16 or fp16 bits, chosen by
+// `bf16_mask` (all ones: bf16), an opaque per-lane value so the choice is a select and not
+// a branch (a branch would split the K loop's basic block).
+template <int SW>
+__device__ __forceinline__ float scale_of(uint32_t b, uint32_t bf16_mask) {
+  if constexpr (SW == 32) {
+    return __builtin_bit_cast(float, b);
+  } else {
+    const uint32_t bf = b << 16;
+    const uint32_t hf = __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)b));
+    return __builtin_bit_cast(float, (bf16_mask & bf) | (~bf16_mask & hf));
+  }
 }
 
-// codes: the role's rows (code bytes); sc: the role's scales. Row n, K offset kc.
-template <int BITS>
-__device__ __forceinline__ BStep b_load(rsrc_t codes, rsrc_t sc, uint32_t row_bytes,
-                                        uint32_t row_groups, int sb, int n, int kc, int gshift) {
-  BStep r;
-  r.q = bload16(codes, (uint32_t)n * row_bytes + (uint32_t)kc * BITS / 8);
-  const uint32_t si = (uint32_t)n * row_groups + ((uint32_t)kc >> gshift);
-  r.s = sb == 4 ? __builtin_amdgcn_raw_buffer_load_b32(sc, si * 4u, 0, 0)
-                : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sc, si * 2u, 0, 0);
+// One role of one expert as a lane reads it: codes and scales (buffer descriptors), the
+// lane's weight row n (clamped into range).
+struct Role {
+  rsrc_t codes, sc;
+  uint32_t row_bytes, row_groups;
+  uint32_t bf16_mask;
+  int n, gshift;
+};
+
+template <int SW>
+__device__ __forceinline__ Role make_role(const char* pk, int64_t w_off, const char* sc,
+                                          int64_t s_off, int rows, int k, int bits, int gshift,
+                                          int sc_dt, int n) {
+  Role r;
+  constexpr int sb = SW / 8;
+  r.row_bytes = (uint32_t)k * bits / 8;
+  r.row_groups = (uint32_t)k >> gshift;
+  r.codes = rsrc(pk + w_off * 4, r.row_bytes * (uint32_t)rows);
+  r.sc = rsrc(sc + s_off * sb, r.row_groups * (uint32_t)rows * sb);
+  r.bf16_mask = opaque(sc_dt == DT_BF16 ? 0xFFFFFFFFu : 0u);
+  r.n = n;
+  r.gshift = gshift;
   return r;
 }
 
-template <int BITS, int ACT>
-__global__ void __launch_bounds__(256)
-prefill_gate_up_kernel(const void* __restrict__ x, uint32_t x_bytes, const int64_t* __restrict__ rows,
-                       const int64_t* __restrict__ tbl, void* __restrict__ h, int n_blocks,
-                       int n_tiles, int top_k, int hidden, int inter, int gshift, int sc_dt,
-                       int64_t gate_w, int64_t gate_s, int64_t up_w, int64_t up_s) {
-  constexpr int CPU = 128 / BITS;                   // codes per lane per K step
-  constexpr int NM = CPU / 8;                       // MFMAs per K step per sub-tile
-  constexpr int KS = 4 * CPU;                       // codes per K step
-  constexpr int LROW = KS * 2 + kStride;            // LDS bytes per staged row
-  __shared__ __align__(16) char lds[kRun * 16 * LROW];
-  int b, tile;
-  item_of(blockIdx.x, n_tiles, b, tile);
-  const RunInfo run = run_of(tbl, b, n_blocks);
-  if (!run.lead) return;
-  const int S = run.nblk;
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int q = lane >> 4, m = lane & 15;
-  const int n = tile * 64 + wv * 16 + m;            // weight row (output column) of lane m
-  const bool n_ok = n < inter;
-  const int nn = n_ok ? n : 0;
-  const char* pk = (const char*)tbl[2 * b];
-  const char* sc = (const char*)tbl[2 * b + 1];
-  const int sb = sc_dt == DT_FP32 ? 4 : 2;
-  const uint32_t row_bytes = (uint32_t)hidden * BITS / 8;
-  const uint32_t row_groups = (uint32_t)hidden >> gshift;
-  const uint32_t role_bytes = row_bytes * (uint32_t)inter;
-  const uint32_t role_sc = row_groups * (uint32_t)inter * sb;
-  const rsrc_t G = rsrc(pk + gate_w * 4, role_bytes), U = rsrc(pk + up_w * 4, role_bytes);
-  const rsrc_t GS = rsrc(sc + gate_s * sb, role_sc), US = rsrc(sc + up_s * sb, role_sc);
-  const rsrc_t X = rsrc(x, x_bytes);
-  const int64_t* rrow = rows + (int64_t)b * 16;
-  AStage<KS> a;
-  a_plan<KS>(a, S, [&](int r) -> uint32_t {
-    const int64_t rid = rrow[r];
-    return rid >= 0 ? (uint32_t)(rid / top_k) * (uint32_t)hidden * 2u : kNoRow;
-  });
-  const Masks M = make_masks();
-  f32x4 ag[kRun], au[kRun];
-#pragma unroll
-  for (int s = 0; s < kRun; ++s) {
-    ag[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    au[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  }
-  a_load<KS>(a, X, S, 0);
-  BStep bg = b_load<BITS>(G, GS, row_bytes, row_groups, sb, nn, q * CPU, gshift);
-  BStep bu = b_load<BITS>(U, US, row_bytes, row_groups, sb, nn, q * CPU, gshift);
-  for (int k0 = 0; k0 < hidden; k0 += KS) {
-    __syncthreads();                                 // previous step's LDS reads are done
-    a_store<KS>(a, lds, S);
-    const int kn = k0 + KS;
-    if (kn < hidden) a_load<KS>(a, X, S, kn);
-    uint4 og[NM], ou[NM];
-    unit_operands<BITS, ACT>(bg.q, round_act<ACT>(scale_of(bg.s, sc_dt)), M, og);
-    unit_operands<BITS, ACT>(bu.q, round_act<ACT>(scale_of(bu.s, sc_dt)), M, ou);
-    if (kn < hidden) {
-      bg = b_load<BITS>(G, GS, row_bytes, row_groups, sb, nn, kn + q * CPU, gshift);
-      bu = b_load<BITS>(U, US, row_bytes, row_groups, sb, nn, kn + q * CPU, gshift);
-    }
-    __syncthreads();                                 // this step's rows are in LDS
-#pragma unroll
-    for (int s = 0; s < kRun; ++s) {
-      if (s < S) {
-#pragma unroll
-        for (int i = 0; i < NM; ++i) {
-          const uint4 av = *(const uint4*)(lds + (s * 16 + m) * LROW + (q * CPU + 8 * i) * 2);
-          ag[s] = mfma16<ACT>(av, og[i], ag[s]);
-          au[s] = mfma16<ACT>(av, ou[i], au[s]);
-        }
-      }
-    }
-  }
-  // C layout: lane (q, m) holds rows 4q..4q+3 of sub-tile s, column m.
-#pragma unroll
-  for (int s = 0; s < kRun; ++s) {
-    if (s < S) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t r = rrow[s * 16 + 4 * q + i];
-        if (r >= 0 && n_ok) store_act<ACT>(h, r * inter + n, silu_mul<ACT>(ag[s][i], au[s][i]));
-      }
-    }
-  }
+template <int BITS, int SW>
+__device__ __forceinline__ BStep b_load(const Role& r, int kc) {
+  BStep o;
+  o.q = bload16(r.codes, (uint32_t)r.n * r.row_bytes + (uint32_t)kc * BITS / 8);
+  const uint32_t si = (uint32_t)r.n * r.row_groups + ((uint32_t)kc >> r.gshift);
+  if constexpr (SW == 32) o.s = __builtin_amdgcn_raw_buffer_load_b32(r.sc, si * 4u, 0, 0);
+  else o.s = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r.sc, si * 2u, 0, 0);
+  return o;
 }
 
-template <int BITS, int ACT>
-__global__ void __launch_bounds__(256)
-prefill_down_kernel(const void* __restrict__ h, uint32_t h_bytes, const int64_t* __restrict__ rows,
-                    const int64_t* __restrict__ tbl, const void* __restrict__ rw, int rw_dt,
-                    float* __restrict__ y, int n_blocks, int n_tiles, int hidden, int inter,
-                    int gshift, int sc_dt, int64_t down_w, int64_t down_s, int w_round) {
+// One K step: the MFMAs of this step (rows in `cur`, B operands `o`) with the dequant of
+// the next step's operands (from `raw`, into `on`) spread over them in program order:
+// operand (r, i) of the next step is built after MFMA slot (r*NM + i) * SLOTS / JOBS.
+template <int BITS, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void k_step(const char* cur, const uint4 (&o)[NR][128 / BITS / 8],
+                                       const BStep (&raw)[NR], const Role (&role)[NR],
+                                       uint4 (&on)[NR][128 / BITS / 8], const Masks& M, int q,
+                                       int m, f32x4 (&acc)[NR][S]) {
   constexpr int CPU = 128 / BITS;
   constexpr int NM = CPU / 8;
   constexpr int KS = 4 * CPU;
-  constexpr int LROW = KS * 2 + kStride;
-  __shared__ __align__(16) char lds[kRun * 16 * LROW];
-  int b, tile;
-  item_of(blockIdx.x, n_tiles, b, tile);
-  const RunInfo run = run_of(tbl, b, n_blocks);
-  if (!run.lead) return;
-  const int S = run.nblk;
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int SLOTS = S * NM, JOBS = NR * NM;
+  float sn[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) sn[r] = round_act<ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask));
+#pragma unroll
+  for (int g = 0; g < SLOTS; ++g) {
+    const int s = g / NM, i = g % NM;
+    const uint4 av = a_read<KS, S, CPU>(cur, s, i, q, m);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r][s] = mfma16<ACT>(av, o[r][i], acc[r][s]);
+#pragma unroll
+    for (int j = g * JOBS / SLOTS; j < (g + 1) * JOBS / SLOTS; ++j)
+      operand_of<BITS, ACT>(raw[j / NM].q, sn[j / NM], M, j % NM, on[j / NM][j % NM]);
+  }
+}
+
+// The K loop of one run: NR roles sharing the activation rows (gate/up: 2, down: 1), S
+// sub-tiles of 16 rows; acc[r][s] is the 16x16 fp32 tile of role r, sub-tile s.
+//
+// Pipeline (two LDS tiles, lds0 and lds1, one step each; the loop runs two steps per
+// iteration so every access names its tile at compile time): step t's rows are in one
+// tile and its B operands are dequantized; the other tile receives step t+1's rows by
+// direct loads issued before step t's MFMAs; the codes of step t+2 are requested after
+// them. At the end of the step one barrier (its wait also covers the direct loads) makes
+// step t+1's rows visible and frees step t's tile. Requests past the last step re-read the
+// last step (no branches in the loop body; their results are not used).
+template <int BITS, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
+                                      const AStage<512 / BITS, S>& a, char* lds0, char* lds1,
+                                      int K, int q, int m, f32x4 (&acc)[NR][S]) {
+  constexpr int CPU = 128 / BITS;
+  constexpr int NM = CPU / 8;
+  constexpr int KS = 4 * CPU;
+  const Masks M = make_masks();
+  const int last = K - KS;
+  uint4 oa[NR][NM], ob[NR][NM];
+  BStep raw[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[r][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  a_issue<KS, S>(a, src, lds0, 0);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], q * CPU);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int i = 0; i < NM; ++i)
+      operand_of<BITS, ACT>(raw[r].q, round_act<ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask)),
+                            M, i, oa[r][i]);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(KS, last) + q * CPU);
+  int k0 = 0;
+  for (; k0 + KS < K; k0 += 2 * KS) {
+    // step k0 (tile lds0, operands oa) -> step k0 + KS (tile lds1, operands ob)
+    a_issue<KS, S>(a, src, lds1, k0 + KS);
+    k_step<BITS, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 2 * KS, last) + q * CPU);
+    __syncthreads();
+    // step k0 + KS (tile lds1, operands ob) -> step k0 + 2 KS (tile lds0, operands oa)
+    a_issue<KS, S>(a, src, lds0, min(k0 + 2 * KS, last));
+    k_step<BITS, ACT, SW, NR, S>(lds1, ob, raw, role, oa, M, q, m, acc);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 3 * KS, last) + q * CPU);
+    __syncthreads();
+  }
+  if (k0 < K)                                      // an odd number of steps: the last one
+    k_step<BITS, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
+}
+
+struct Item {
+  int b, tile, S;
+};
+
+// This workgroup's run and N tile, or S = 0 when it has none.
+template <int R>
+__device__ __forceinline__ Item item_here(const int64_t* tbl, int n_blocks, int n_tiles) {
+  Item it;
+  item_of<R>(blockIdx.x, n_tiles, it.b, it.tile);
+  const RunInfo run = run_of<R>(tbl, it.b, n_blocks);
+  it.S = run.lead ? run.nblk : 0;
+  return it;
+}
+
+template <int BITS, int ACT, int SW, int S>
+__device__ __forceinline__ void gate_up_run(const Item& it, const void* x,
+                                            const int64_t* rows, const int64_t* tbl, void* h,
+                                            int top_k, int hidden, int inter, int gshift,
+                                            int sc_dt, int64_t gate_w, int64_t gate_s,
+                                            int64_t up_w, int64_t up_s, char* lds0,
+                                            char* lds1) {
+  constexpr int KS = 512 / BITS;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int q = lane >> 4, m = lane & 15;
-  const int n = tile * 64 + wv * 16 + m;
+  const int n = it.tile * kTileN + wv * 16 + m;         // weight row (output column) of lane m
+  const bool n_ok = n < inter;
+  const int nn = n_ok ? n : 0;
+  const char* pk = (const char*)tbl[2 * it.b];
+  const char* sc = (const char*)tbl[2 * it.b + 1];
+  const Role role[2] = {make_role<SW>(pk, gate_w, sc, gate_s, inter, hidden, BITS, gshift, sc_dt, nn),
+                        make_role<SW>(pk, up_w, sc, up_s, inter, hidden, BITS, gshift, sc_dt, nn)};
+  const int64_t* rrow = rows + (int64_t)it.b * 16;
+  AStage<KS, S> a;
+  a_plan<KS, S>(a, [&](int r) -> uint32_t {
+    const int64_t rid = rrow[r];
+    return rid >= 0 ? (uint32_t)(rid / top_k) * (uint32_t)hidden * 2u : kNoRow;
+  });
+  f32x4 acc[2][S];
+  run_k<BITS, ACT, SW, 2, S>(role, rsrc(x, kNoRow), a, lds0, lds1, hidden, q, m, acc);
+  // C layout: lane (q, m) holds rows 4q..4q+3 of sub-tile s, column m.
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = rrow[s * 16 + 4 * q + i];
+      if (r >= 0 && n_ok) store_act<ACT>(h, r * inter + n, silu_mul<ACT>(acc[0][s][i], acc[1][s][i]));
+    }
+}
+
+template <int BITS, int ACT, int SW, int S>
+__device__ __forceinline__ void down_run(const Item& it, const void* h, const int64_t* rows,
+                                         const int64_t* tbl, const void* rw, int rw_dt, float* y,
+                                         int hidden, int inter, int gshift, int sc_dt,
+                                         int64_t down_w, int64_t down_s, int w_round,
+                                         char* lds0, char* lds1) {
+  constexpr int KS = 512 / BITS;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int q = lane >> 4, m = lane & 15;
+  const int n = it.tile * kTileN + wv * 16 + m;
   const bool n_ok = n < hidden;
   const int nn = n_ok ? n : 0;
-  const char* pk = (const char*)tbl[2 * b];
-  const char* sc = (const char*)tbl[2 * b + 1];
-  const int sb = sc_dt == DT_FP32 ? 4 : 2;
-  const uint32_t row_bytes = (uint32_t)inter * BITS / 8;
-  const uint32_t row_groups = (uint32_t)inter >> gshift;
-  const rsrc_t D = rsrc(pk + down_w * 4, row_bytes * (uint32_t)hidden);
-  const rsrc_t DS = rsrc(sc + down_s * sb, row_groups * (uint32_t)hidden * sb);
-  const rsrc_t HB = rsrc(h, h_bytes);
-  const int64_t* rrow = rows + (int64_t)b * 16;
-  AStage<KS> a;
-  a_plan<KS>(a, S, [&](int r) -> uint32_t {
+  const char* pk = (const char*)tbl[2 * it.b];
+  const char* sc = (const char*)tbl[2 * it.b + 1];
+  const Role role[1] = {make_role<SW>(pk, down_w, sc, down_s, hidden, inter, BITS, gshift, sc_dt, nn)};
+  const int64_t* rrow = rows + (int64_t)it.b * 16;
+  AStage<KS, S> a;
+  a_plan<KS, S>(a, [&](int r) -> uint32_t {
     const int64_t rid = rrow[r];
     return rid >= 0 ? (uint32_t)rid * (uint32_t)inter * 2u : kNoRow;
   });
-  const Masks M = make_masks();
-  f32x4 acc[kRun];
+  f32x4 acc[1][S];
+  run_k<BITS, ACT, SW, 1, S>(role, rsrc(h, kNoRow), a, lds0, lds1, inter, q, m, acc);
 #pragma unroll
-  for (int s = 0; s < kRun; ++s) acc[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  a_load<KS>(a, HB, S, 0);
-  BStep bd = b_load<BITS>(D, DS, row_bytes, row_groups, sb, nn, q * CPU, gshift);
-  for (int k0 = 0; k0 < inter; k0 += KS) {
-    __syncthreads();
-    a_store<KS>(a, lds, S);
-    const int kn = k0 + KS;
-    if (kn < inter) a_load<KS>(a, HB, S, kn);
-    uint4 od[NM];
-    unit_operands<BITS, ACT>(bd.q, round_act<ACT>(scale_of(bd.s, sc_dt)), M, od);
-    if (kn < inter) bd = b_load<BITS>(D, DS, row_bytes, row_groups, sb, nn, kn + q * CPU, gshift);
-    __syncthreads();
+  for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int s = 0; s < kRun; ++s) {
-      if (s < S) {
-#pragma unroll
-        for (int i = 0; i < NM; ++i) {
-          const uint4 av = *(const uint4*)(lds + (s * 16 + m) * LROW + (q * CPU + 8 * i) * 2);
-          acc[s] = mfma16<ACT>(av, od[i], acc[s]);
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = rrow[s * 16 + 4 * q + i];
+      if (r >= 0 && n_ok) {
+        float c = round_act<ACT>(acc[0][s][i]) * load_dt(rw, r, rw_dt);
+        if (w_round) c = round_act<ACT>(c);
+        y[r * hidden + n] = c;
       }
     }
-  }
-#pragma unroll
-  for (int s = 0; s < kRun; ++s) {
-    if (s < S) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t r = rrow[s * 16 + 4 * q + i];
-        if (r >= 0 && n_ok) {
-          float c = round_act<ACT>(acc[s][i]) * load_dt(rw, r, rw_dt);
-          if (w_round) c = round_act<ACT>(c);
-          y[r * hidden + n] = c;
-        }
-      }
-    }
-  }
 }
+
+#define VAAYU_BY_S4(CALL)                                                          \
+  switch (it.S) {                                                                   \
+    case 1: CALL(1); break; case 2: CALL(2); break; case 3: CALL(3); break;          \
+    case 4: CALL(4); break; default: break;                                         \
+  }
+#define VAAYU_BY_S8(CALL)                                                          \
+  switch (it.S) {                                                                   \
+    case 1: CALL(1); break; case 2: CALL(2); break; case 3: CALL(3); break;          \
+    case 4: CALL(4); break; case 5: CALL(5); break; case 6: CALL(6); break;          \
+    case 7: CALL(7); break; case 8: CALL(8); break; default: break;                 \
+  }
+
+template <int BITS, int ACT, int SW>
+__global__ void __launch_bounds__(64 * kWaves)
+prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ rows,
+                       const int64_t* __restrict__ tbl, void* __restrict__ h, int n_blocks,
+                       int n_tiles, int top_k, int hidden, int inter, int gshift, int sc_dt,
+                       int64_t gate_w, int64_t gate_s, int64_t up_w, int64_t up_s) {
+  __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / BITS)];
+  const Item it = item_here<kRunGateUp>(tbl, n_blocks, n_tiles);
+#define GU_CALL(S_) gate_up_run<BITS, ACT, SW, S_>(it, x, rows, tbl, h, top_k, hidden, inter, gshift, \
+                                               sc_dt, gate_w, gate_s, up_w, up_s, lds0, lds1)
+  VAAYU_BY_S8(GU_CALL)
+#undef GU_CALL
+}
+
+template <int BITS, int ACT, int SW>
+__global__ void __launch_bounds__(64 * kWaves)
+prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows,
+                    const int64_t* __restrict__ tbl, const void* __restrict__ rw, int rw_dt,
+                    float* __restrict__ y, int n_blocks, int n_tiles, int hidden, int inter,
+                    int gshift, int sc_dt, int64_t down_w, int64_t down_s, int w_round) {
+  __shared__ __align__(1024) char lds0[kRunDown * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / BITS)];
+  const Item it = item_here<kRunDown>(tbl, n_blocks, n_tiles);
+#define DN_CALL(S_) down_run<BITS, ACT, SW, S_>(it, h, rows, tbl, rw, rw_dt, y, hidden, inter, gshift, \
+                                            sc_dt, down_w, down_s, w_round, lds0, lds1)
+  VAAYU_BY_S8(DN_CALL)
+#undef DN_CALL
+}
+
+#undef VAAYU_BY_S4
+#undef VAAYU_BY_S8
 
 // out[t, c] = sum_k y[ord[t*top_k + k], c], sequential from 0.
 __global__ void __launch_bounds__(256)
@@ -417,19 +532,21 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
   if (n_blocks <= 0 || top_k <= 0) return set_error(-1, "n_blocks / top_k must be positive");
   if (scale_dtype < 0 || scale_dtype > 2) return set_error(-1, "scale dtype");
   if (const char* why = prefill_unsupported(g, act)) return set_error(-2, why);
-  const int n_tiles = (g->inter + 63) / 64;
+  const int n_tiles = (g->inter + kTileN - 1) / kTileN;
   int gshift = 0;
   while ((1 << gshift) < g->group) ++gshift;
-  const dim3 grid((unsigned)items_for(n_blocks, n_tiles)), block(256);
+  const dim3 grid((unsigned)items_for<kRunGateUp>(n_blocks, n_tiles)), block(64 * kWaves);
   hipStream_t st = (hipStream_t)stream;
-#define GU(B_, A_)                                                                        \
-  hipLaunchKernelGGL((prefill_gate_up_kernel<B_, A_>), grid, block, 0, st, x, kNoRow, rows,     \
-                     table, h, n_blocks, n_tiles, top_k, g->hidden, g->inter, gshift,         \
-                     scale_dtype, g->gate_w, g->gate_s, g->up_w, g->up_s)
-  if (g->bits == 4 && act == DT_BF16) GU(4, DT_BF16);
-  else if (g->bits == 4) GU(4, DT_FP16);
-  else if (act == DT_BF16) GU(8, DT_BF16);
-  else GU(8, DT_FP16);
+#define GU(B_, A_, W_)                                                                        \
+  hipLaunchKernelGGL((prefill_gate_up_kernel<B_, A_, W_>), grid, block, 0, st, x, rows, table, h, \
+                     n_blocks, n_tiles, top_k, g->hidden, g->inter, gshift, scale_dtype,         \
+                     g->gate_w, g->gate_s, g->up_w, g->up_s)
+#define GU2(B_, A_) if (scale_dtype == DT_FP32) GU(B_, A_, 32); else GU(B_, A_, 16)
+  if (g->bits == 4 && act == DT_BF16) { GU2(4, DT_BF16); }
+  else if (g->bits == 4) { GU2(4, DT_FP16); }
+  else if (act == DT_BF16) { GU2(8, DT_BF16); }
+  else { GU2(8, DT_FP16); }
+#undef GU2
 #undef GU
   return check_launch("prefill gate/up");
 }
@@ -445,19 +562,21 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
   if (scale_dtype < 0 || scale_dtype > 2 || rw_dtype < 0 || rw_dtype > 2)
     return set_error(-1, "scale / routing-weight dtype");
   if (const char* why = prefill_unsupported(g, act)) return set_error(-2, why);
-  const int n_tiles = (g->hidden + 63) / 64;
+  const int n_tiles = (g->hidden + kTileN - 1) / kTileN;
   int gshift = 0;
   while ((1 << gshift) < g->group) ++gshift;
-  const dim3 grid((unsigned)items_for(n_blocks, n_tiles)), block(256);
+  const dim3 grid((unsigned)items_for<kRunDown>(n_blocks, n_tiles)), block(64 * kWaves);
   hipStream_t st = (hipStream_t)stream;
-#define DN(B_, A_)                                                                          \
-  hipLaunchKernelGGL((prefill_down_kernel<B_, A_>), grid, block, 0, st, h, kNoRow, rows, table, \
-                     routing_weights, rw_dtype, y, n_blocks, n_tiles, g->hidden, g->inter,      \
+#define DN(B_, A_, W_)                                                                          \
+  hipLaunchKernelGGL((prefill_down_kernel<B_, A_, W_>), grid, block, 0, st, h, rows, table,         \
+                     routing_weights, rw_dtype, y, n_blocks, n_tiles, g->hidden, g->inter,          \
                      gshift, scale_dtype, g->down_w, g->down_s, w_round)
-  if (g->bits == 4 && act == DT_BF16) DN(4, DT_BF16);
-  else if (g->bits == 4) DN(4, DT_FP16);
-  else if (act == DT_BF16) DN(8, DT_BF16);
-  else DN(8, DT_FP16);
+#define DN2(B_, A_) if (scale_dtype == DT_FP32) DN(B_, A_, 32); else DN(B_, A_, 16)
+  if (g->bits == 4 && act == DT_BF16) { DN2(4, DT_BF16); }
+  else if (g->bits == 4) { DN2(4, DT_FP16); }
+  else if (act == DT_BF16) { DN2(8, DT_BF16); }
+  else { DN2(8, DT_FP16); }
+#undef DN2
 #undef DN
   return check_launch("prefill down");
 }
