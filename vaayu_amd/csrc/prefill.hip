@@ -336,14 +336,17 @@ __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
   for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(KS, last) + q * CPU);
   int k0 = 0;
   for (; k0 + KS < K; k0 += 2 * KS) {
-    // step k0 (tile lds0, operands oa) -> step k0 + KS (tile lds1, operands ob)
+    // step k0 (tile lds0, operands oa) -> step k0 + KS (tile lds1, operands ob); the
+    // scheduling barriers keep the next step's loads ahead of this step's MFMAs
     a_issue<KS, S>(a, src, lds1, k0 + KS);
+    __builtin_amdgcn_sched_barrier(0);
     k_step<BITS, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 2 * KS, last) + q * CPU);
     __syncthreads();
     // step k0 + KS (tile lds1, operands ob) -> step k0 + 2 KS (tile lds0, operands oa)
     a_issue<KS, S>(a, src, lds0, min(k0 + 2 * KS, last));
+    __builtin_amdgcn_sched_barrier(0);
     k_step<BITS, ACT, SW, NR, S>(lds1, ob, raw, role, oa, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 3 * KS, last) + q * CPU);
