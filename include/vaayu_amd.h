@@ -21,9 +21,23 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 1
+#define VAAYU_ABI_VERSION 2
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
+
+/* Scale dtype code for E8M0 exponent bytes (MXFP4 scales). */
+enum { VAAYU_E8M0 = 3 };
+
+/* Code formats of an expert blob. VAAYU_FMT_INT: the reference's packed unsigned integer
+ * codes (`bits` wide, offset 2^(bits-1)), `group` codes per scale along a row. VAAYU_FMT_E4M3:
+ * float8 e4m3fn codes (bits = 8), one fp32 scale per block_rows x group tile, the weight
+ * fp32(code) * scale rounded to the activation dtype, as `dequantize_block_scaled`
+ * (vaayu/model_code/deepseek_v4/modeling_deepseek_v4.py:228-240). VAAYU_FMT_MXFP4: e2m1
+ * codes (bits = 4, even element in the low nibble), one E8M0 scale per 32 codes along a
+ * row, as `upcast_from_mxfp_torch` (vendor gpt_oss_triton_kernels
+ * numerics_details/mxfp.py:256-299). Codes are packed along the last dim in 32-bit words,
+ * roles gate, down, up in that order, like the reference's int blobs. */
+enum { VAAYU_FMT_INT = 0, VAAYU_FMT_E4M3 = 1, VAAYU_FMT_MXFP4 = 2 };
 
 /* One packed expert blob's geometry: `geom = (bits, group, roles)` and the per-role
  * (word offset, scale offset) that `_layout` derives from it
@@ -37,10 +51,15 @@ typedef struct vaayu_geom {
     int64_t gate_w, gate_s;
     int64_t up_w, up_s;
     int64_t down_w, down_s;
+    int32_t format;      /* VAAYU_FMT_* */
+    int32_t block_rows;  /* rows per scale (VAAYU_FMT_E4M3), else 1 */
 } vaayu_geom;
 
 int vaayu_abi_version(void);
 const char *vaayu_last_error(void);
+
+/* The decode entries take every code format above, scale_dtype 0 bf16, 1 fp16, 2 fp32 or
+ * 3 E8M0; the prefill entries take VAAYU_FMT_INT. */
 
 /* Decode, gate/up stage. Replaces `_gate_up` / `_gate_up_kernel`
  * (vaayu/packed_expert_kernels.py:355-371, 131-150).

@@ -245,12 +245,44 @@ def expert_weights(blob: dict, act) -> tuple:
     if "dense" in blob:
         d = blob["dense"]
         return tuple(round_to(to_np(d[r]), act_name(act)) for r in ("gate", "down", "up"))
+    if isinstance(blob["geom"][0], str):
+        return format_expert_weights(blob, act)
     bits, gs, roles = blob["geom"]
     flat = dequant_flat(blob["flat"]["packed"], blob["flat"]["scale"], bits, gs, act)
     out, at = {}, 0
     for role, rows, cols in roles:
         out[role] = flat[at:at + rows * cols].reshape(rows, cols)
         at += rows * cols
+    return out["gate"], out["down"], out["up"]
+
+
+def format_expert_weights(blob: dict, act) -> tuple:
+    """(w_gate, w_down, w_up) of an FP8 ("e4m3", (bo, bi)) or MXFP4 ("mxfp4", 32) blob:
+    roles gate, down, up concatenated, codes along the last dim; each role through
+    `dequant_block_scaled` / `upcast_mxfp4` (the weights the reference's dequant of that
+    format gives: vaayu/model_code/deepseek_v4/modeling_deepseek_v4.py:228-240, vendor
+    …/numerics_details/mxfp.py:256-299)."""
+    act = act_name(act)
+    kind, gs, roles = blob["geom"]
+    codes = to_np(blob["flat"]["packed"]).astype(np.int32).view(np.uint8)
+    scale = to_np(blob["flat"]["scale"])
+    out, c_at, s_at = {}, 0, 0
+    for role, rows, cols in roles:
+        if kind == "e4m3":
+            bo, bi = gs
+            n_c, n_s = rows * cols, (rows // bo) * (cols // bi)
+            q = codes[c_at:c_at + n_c].reshape(rows, cols)
+            sc = scale[s_at:s_at + n_s].astype(np.float32).reshape(rows // bo, cols // bi)
+            out[role] = dequant_block_scaled(q, sc, act)
+        elif kind == "mxfp4":
+            n_c, n_s = rows * cols // 2, rows * cols // 32
+            q = codes[c_at:c_at + n_c].reshape(rows, cols // 2)
+            sc = scale[s_at:s_at + n_s].astype(np.uint8).reshape(rows, cols // 32)
+            out[role] = upcast_mxfp4(q, sc, act)
+        else:
+            raise ValueError(f"format {kind!r}")
+        c_at += n_c
+        s_at += n_s
     return out["gate"], out["down"], out["up"]
 
 

@@ -67,3 +67,27 @@ def rel(a, b):
 
 def frac_equal(a, b):
     return O.isclose_frac(O.to_np(a), O.to_np(b))
+
+
+@functools.lru_cache(maxsize=None)
+def format_blobs(fmt, hid, inter, k, device="cuda"):
+    """k distinct FP8 ("e4m3", 128 x 128 fp32 block scales) or MXFP4 ("mxfp4", E8M0 per 32)
+    expert blobs of N(0, 0.05) weights, built on the CPU and copied to `device`."""
+    from vaayu_amd.block_formats import random_format_expert
+    g = torch.Generator().manual_seed(hid * 3 + inter + len(fmt))
+    blobs = [random_format_expert(fmt, hid, inter, generator=g, device="cpu", std=0.05)
+             for _ in range(k)]
+    return tuple(to_device(b, device) for b in blobs)
+
+
+def format_case(fmt, hid, inter, k, seed=0, w_dtype=torch.float32, act=torch.bfloat16):
+    """(x, pairs, routing_weights, cpu_pairs) over `format_blobs`, as `decode_case`."""
+    blobs = format_blobs(fmt, hid, inter, k)
+    cb = format_blobs(fmt, hid, inter, k, "cpu")
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(1, hid, generator=g) * 0.5).to(act)
+    w = torch.rand(1, k, generator=g) + 0.05
+    w = (w / w.sum(-1, keepdim=True)).to(w_dtype)
+    slots = torch.randperm(k, generator=torch.Generator().manual_seed(seed)).tolist()
+    return (x.cuda(), [(blobs[i], slots[i]) for i in range(k)], w.cuda(),
+            [(cb[i], slots[i]) for i in range(k)])

@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -26,7 +26,8 @@ class Geom(ctypes.Structure):
                 ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
                 ("gate_w", ctypes.c_int64), ("gate_s", ctypes.c_int64),
                 ("up_w", ctypes.c_int64), ("up_s", ctypes.c_int64),
-                ("down_w", ctypes.c_int64), ("down_s", ctypes.c_int64)]
+                ("down_w", ctypes.c_int64), ("down_s", ctypes.c_int64),
+                ("format", ctypes.c_int32), ("block_rows", ctypes.c_int32)]
 
 
 class KernelError(RuntimeError):
@@ -93,13 +94,11 @@ def stream_ptr(device=None) -> int:
 
 
 def geom_struct(geom) -> Geom:
-    """`vaayu_geom` for a blob geometry `(bits, gs, roles)` via `_layout`."""
-    bits, gs, roles = geom
-    lay, w_at, s_at = {}, 0, 0
-    for role, rows, cols in roles:
-        lay[role] = (w_at, s_at, rows, cols)
-        w_at += rows * cols * bits // 32
-        s_at += rows * cols // gs
+    """`vaayu_geom` for a blob geometry `(bits or format, gs, roles)`: the role offsets of
+    `_layout`, the code format and its scale blocking."""
+    from .block_formats import blob_layout, geom_format
+    fmt, bits, group, brows = geom_format(geom)
+    lay = blob_layout(geom)
     inter, hidden = lay["gate"][2], lay["gate"][3]
-    return Geom(bits, gs, hidden, inter, lay["gate"][0], lay["gate"][1], lay["up"][0],
-                lay["up"][1], lay["down"][0], lay["down"][1])
+    return Geom(bits, group, hidden, inter, lay["gate"][0], lay["gate"][1], lay["up"][0],
+                lay["up"][1], lay["down"][0], lay["down"][1], fmt, brows)

@@ -129,3 +129,118 @@ def upcast_from_mxfp(tensor: torch.Tensor, scale: torch.Tensor, target_dtype: to
 
 
 upcast_from_mxfp_torch = upcast_from_mxfp
+
+
+# ── FP8 / MXFP4 expert blobs ────────────────────────────────────────────────────────────
+#
+# The reference keeps packed experts as {"flat": {"packed", "scale"}, "geom": (bits, gs,
+# roles)} (vaayu/moe_patch.py:794-846). FP8 and MXFP4 experts use the same container: the
+# roles gate, down, up concatenated, codes along the last dim in int32 words, and geom
+#   ("e4m3", (bo, bi), roles)  float8_e4m3fn codes, one fp32 scale per bo x bi tile
+#   ("mxfp4", 32, roles)       e2m1 codes (even element in the low nibble), one E8M0 byte
+#                              per 32 codes along a row
+# so the pointer tables, layout arithmetic and kernels take them like the int blobs.
+
+FMT_INT, FMT_E4M3, FMT_MXFP4 = 0, 1, 2
+
+
+def geom_format(geom):
+    """(format code, code bits, codes per scale along a row, rows per scale) of a blob
+    geometry."""
+    kind, gs, _roles = geom
+    if kind == "e4m3":
+        bo, bi = gs
+        return FMT_E4M3, 8, int(bi), int(bo)
+    if kind == "mxfp4":
+        return FMT_MXFP4, 4, 32, 1
+    return FMT_INT, int(kind), int(gs), 1
+
+
+def blob_layout(geom) -> dict:
+    """{role: (word offset, scale offset, rows, cols)} in the flat streams, for every
+    format (the int case is the reference's `_layout`, vaayu/packed_expert_kernels.py:301-309)."""
+    _fmt, bits, group, brows = geom_format(geom)
+    out, w_at, s_at = {}, 0, 0
+    for role, rows, cols in geom[2]:
+        out[role] = (w_at, s_at, rows, cols)
+        w_at += rows * cols * bits // 32
+        s_at += (rows // brows) * (cols // group)
+    return out
+
+
+def _fp8_codes(w: torch.Tensor, block) -> tuple:
+    """(e4m3 codes, fp32 scales) of one role: scale = amax / 448 per block (1 for an
+    all-zero block), codes = the e4m3 cast of w / scale."""
+    bo, bi = block
+    rows, cols = w.shape
+    t = w.float().reshape(rows // bo, bo, cols // bi, bi)
+    amax = t.abs().amax(dim=(1, 3))
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (t / scale[:, None, :, None]).reshape(rows, cols).to(torch.float8_e4m3fn)
+    return q, scale.float()
+
+
+_E2M1_GRID = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def _mxfp4_codes(w: torch.Tensor) -> tuple:
+    """(e2m1 codes as uint8 pairs [rows, cols/2], E8M0 scales [rows, cols/32]) of one role:
+    per 32 along a row, the scale exponent makes the block's amax at most 6, each value
+    rounded to the nearest e2m1 magnitude (ties to the even code)."""
+    rows, cols = w.shape
+    t = w.float().reshape(rows, cols // 32, 32)
+    amax = t.abs().amax(dim=-1)
+    e = torch.where(amax > 0, torch.ceil(torch.log2(amax / 6.0)), torch.full_like(amax, -127))
+    e = e.clamp(-127, 127)
+    scale = torch.pow(2.0, e)
+    v = (t / scale[..., None]).clamp(-6.0, 6.0)
+    grid = _E2M1_GRID.to(v.device)
+    mag = (v.abs()[..., None] - grid).abs()
+    best = mag.argmin(dim=-1)                                   # lowest code on ties
+    code = best + torch.where(v < 0, 8, 0)
+    code = torch.where(best == 0, torch.zeros_like(code), code)  # -0 stored as +0
+    code = code.reshape(rows, cols).to(torch.uint8)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).to(torch.uint8)
+    return packed, (e + 127).to(torch.uint8)
+
+
+def random_format_expert(fmt: str, hidden: int, inter: int, *, generator, device,
+                         std: float = 0.02) -> dict:
+    """A synthetic FP8 ("e4m3", 128 x 128 fp32 block scales) or MXFP4 ("mxfp4") expert blob
+    of bf16 N(0, std) weights, roles gate, down, up."""
+    roles = (("gate", inter, hidden), ("down", hidden, inter), ("up", inter, hidden))
+    packed, scales = [], []
+    for _role, rows, cols in roles:
+        w = (torch.randn(rows, cols, generator=generator, device=device) * std).to(torch.bfloat16)
+        if fmt == "e4m3":
+            q, s = _fp8_codes(w, (128, 128))
+            packed.append(q.view(torch.uint8).reshape(-1))
+        elif fmt == "mxfp4":
+            q, s = _mxfp4_codes(w)
+            packed.append(q.reshape(-1))
+        else:
+            raise ValueError(f"format {fmt}")
+        scales.append(s.reshape(-1))
+    words = torch.cat(packed).contiguous().view(torch.int32)
+    geom = ("e4m3", (128, 128), roles) if fmt == "e4m3" else ("mxfp4", 32, roles)
+    return {"flat": {"packed": words, "scale": torch.cat(scales).contiguous()}, "geom": geom}
+
+
+def dequantize_format_blob(blob: dict, dtype: torch.dtype) -> dict:
+    """{role: dense weight} of an FP8 / MXFP4 blob: each role through the mirrors above
+    (HIP on a GPU, the reference's arithmetic on the CPU)."""
+    fmt, _bits, group, brows = geom_format(blob["geom"])
+    lay = blob_layout(blob["geom"])
+    codes = blob["flat"]["packed"].view(torch.uint8)
+    scale = blob["flat"]["scale"]
+    out = {}
+    for role, (w_at, s_at, rows, cols) in lay.items():
+        if fmt == FMT_E4M3:
+            q = codes[w_at * 4: w_at * 4 + rows * cols].view(rows, cols)
+            sc = scale[s_at: s_at + (rows // brows) * (cols // group)].view(rows // brows, cols // group)
+            out[role] = dequantize_block_scaled(q.view(torch.float8_e4m3fn), sc, dtype)
+        else:
+            q = codes[w_at * 4: w_at * 4 + rows * cols // 2].view(rows, cols // 2)
+            sc = scale[s_at: s_at + rows * cols // 32].view(rows, cols // 32)
+            out[role] = upcast_from_mxfp(q, sc, dtype, axis=-1)
+    return out

@@ -19,33 +19,6 @@ namespace vaayu {
 enum { FMT_E2M1 = 0, FMT_E4M3 = 1 };
 enum { SC_BF16 = 0, SC_FP16 = 1, SC_FP32 = 2, SC_E8M0 = 3 };
 
-// float8 e4m3fn (bias 7, no infinities, S.1111.111 is NaN) -> fp32, exact.
-__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
-  const uint32_t sign = (b & 0x80u) << 24;
-  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
-  float mag;
-  if (e == 0) {
-    mag = (float)m * 0x1p-9f;                                   // subnormal: m/8 * 2^-6
-  } else if (e == 15 && m == 7) {
-    mag = __builtin_nanf("");
-  } else {
-    mag = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
-  }
-  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mag) | sign);
-}
-
-// e2m1 nibble (bit 3 the sign; values 0, .5, 1, 1.5, 2, 3, 4, 6) -> fp32, exact.
-__device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
-  const uint32_t sign = (n & 8u) << 28;
-  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
-  const uint32_t mag = e ? (((e + 126u) << 23) | (m << 22)) : (m ? 0x3F000000u : 0u);
-  return __builtin_bit_cast(float, mag | sign);
-}
-
-__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
-  return s == 0xFFu ? __builtin_nanf("") : __builtin_bit_cast(float, s << 23);
-}
-
 template <int SC>
 __device__ __forceinline__ float load_scale(const void* p, int64_t i) {
   if constexpr (SC == SC_E8M0) return e8m0_to_f32(((const uint8_t*)p)[i]);

@@ -200,6 +200,64 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
   }
 }
 
+// ── FP8 / FP4 codes and E8M0 scales ─────────────────────────────────────────────────────
+
+// float8 e4m3fn (bias 7, no infinities, S.1111.111 is NaN) -> fp32, exact.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
+  float mag;
+  if (e == 0) {
+    mag = (float)m * 0x1p-9f;                                   // subnormal: m/8 * 2^-6
+  } else if (e == 15 && m == 7) {
+    mag = __builtin_nanf("");
+  } else {
+    mag = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  }
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mag) | sign);
+}
+
+// e2m1 nibble (bit 3 the sign; values 0, .5, 1, 1.5, 2, 3, 4, 6) -> fp32, exact.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
+  const uint32_t sign = (n & 8u) << 28;
+  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
+  const uint32_t mag = e ? (((e + 126u) << 23) | (m << 22)) : (m ? 0x3F000000u : 0u);
+  return __builtin_bit_cast(float, mag | sign);
+}
+
+// E8M0 scale byte -> the fp32 with exponent bits s (s = 0 gives 0), 0xFF -> NaN.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+  return s == 0xFFu ? __builtin_nanf("") : __builtin_bit_cast(float, s << 23);
+}
+
+// Two fp32 values -> one packed pair of the activation dtype (bf16 or fp16), nearest-even.
+template <int ACT>
+__device__ __forceinline__ uint32_t pack_act(float a, float b) {
+  if constexpr (ACT == DT_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
+
+// e4m3 word (4 codes, code k in byte k) -> 2 packed weight pairs round_act(fp32(c) * s):
+// the fp32 product rounded once, then one rounding to the activation dtype.
+template <int ACT>
+__device__ __forceinline__ void deq_word_e4m3(uint32_t w, float s, uint32_t out[2]) {
+  const float f0 = e4m3_to_f32(w & 0xFFu) * s, f1 = e4m3_to_f32((w >> 8) & 0xFFu) * s;
+  const float f2 = e4m3_to_f32((w >> 16) & 0xFFu) * s, f3 = e4m3_to_f32(w >> 24) * s;
+  out[0] = pack_act<ACT>(f0, f1);
+  out[1] = pack_act<ACT>(f2, f3);
+}
+
+// e2m1 word (8 codes, code k in bits 4k..4k+3) -> 4 packed weight pairs round_act(e2m1 * s).
+template <int ACT>
+__device__ __forceinline__ void deq_word_e2m1(uint32_t w, float s, uint32_t out[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    out[k] = pack_act<ACT>(e2m1_to_f32((w >> (8 * k)) & 0xFu) * s,
+                           e2m1_to_f32((w >> (8 * k + 4)) & 0xFu) * s);
+}
+
 // ── wavefront reductions ───────────────────────────────────────────────────────────────
 
 template <int WIDTH>

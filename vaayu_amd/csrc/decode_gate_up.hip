@@ -37,8 +37,14 @@ static int by_ch(const void* x, const int64_t* tbl, void* h, const DecodeShape& 
 template <int BITS, int ACT>
 static int by_sw(const void* x, const int64_t* tbl, void* h, const DecodeShape& s,
                  const vaayu_geom* g, int sc, hipStream_t st) {
-  if (sc == DT_FP32) return by_ch<BITS, ACT, 32>(x, tbl, h, s, g, st);
-  return by_ch<BITS, ACT, 16>(x, tbl, h, s, g, st);
+  if constexpr (BITS == F_MXFP4) {
+    if (sc == VAAYU_E8M0) return by_ch<BITS, ACT, 8>(x, tbl, h, s, g, st);
+    return set_error(-2, "mxfp4 scales are E8M0");
+  } else {
+    if (sc == VAAYU_E8M0) return set_error(-2, "E8M0 scales go with mxfp4 codes");
+    if (sc == DT_FP32) return by_ch<BITS, ACT, 32>(x, tbl, h, s, g, st);
+    return by_ch<BITS, ACT, 16>(x, tbl, h, s, g, st);
+  }
 }
 
 }  // namespace vaayu
@@ -51,20 +57,22 @@ extern "C" int vaayu_decode_gate_up(const void* x, const int64_t* table, void* h
   clear_error();
   if (!x || !table || !h || !geom) return set_error(-1, "null pointer argument");
   if (n_pairs <= 0) return set_error(-1, "n_pairs must be positive");
-  if (scale_dtype < 0 || scale_dtype > 2) return set_error(-1, "scale dtype");
+  if (scale_dtype < 0 || scale_dtype > 3) return set_error(-1, "scale dtype");
   if (((uintptr_t)x) & 15) return set_error(-1, "x must be 16-byte aligned");
   if (const char* why = decode_unsupported(geom, act)) return set_error(-2, why);
-  const bool fast = (geom->bits == 4 || geom->bits == 8) && act != DT_FP32;
+  const int fmt = code_format(geom);
+  const bool fast = (fmt == 4 || fmt == 8 || fmt >= 100) && act != DT_FP32;
   const Plan pl = plan_row(geom->hidden * geom->bits / 128, 2, 2, fast);
   if (pl.lpr == 0) return set_error(-2, "decode gate/up: no lane split of this row is built");
   const DecodeShape s = shape_for(geom, n_pairs, geom->hidden, geom->inter, scale_dtype, pl);
   hipStream_t st = (hipStream_t)stream;
   int rc;
-#define BA(B_, A_) else if (geom->bits == B_ && act == A_) rc = by_sw<B_, A_>(x, table, h, s, geom, scale_dtype, st);
+#define BA(B_, A_) else if (fmt == B_ && act == A_) rc = by_sw<B_, A_>(x, table, h, s, geom, scale_dtype, st);
   if (false) rc = 0;
   BA(4, 0) BA(4, 1) BA(4, 2) BA(8, 0) BA(8, 1) BA(8, 2) BA(2, 0) BA(2, 1) BA(2, 2)
-  BA(1, 0) BA(1, 1) BA(1, 2)
-  else rc = set_error(-2, "unsupported bit width / activation dtype");
+  BA(1, 0) BA(1, 1) BA(1, 2) BA(F_E4M3, 0) BA(F_E4M3, 1) BA(F_E4M3, 2)
+  BA(F_MXFP4, 0) BA(F_MXFP4, 1) BA(F_MXFP4, 2)
+  else rc = set_error(-2, "unsupported code format / activation dtype");
 #undef BA
   return rc ? rc : check_launch("decode gate/up");
 }

@@ -25,6 +25,18 @@ namespace vaayu {
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
+// Code formats F of the decode kernels: 1, 2, 4, 8 are packed unsigned integers of that
+// many bits (offset 2^(F-1), scale rounded to the activation dtype); F_E4M3 is float8
+// e4m3fn with fp32 block scales, F_MXFP4 is e2m1 with an E8M0 scale per 32 codes (both
+// scales applied unrounded, as the reference's dequant does).
+enum { F_MXFP4 = 104, F_E4M3 = 108 };
+
+template <int F>
+struct CodeBits {
+  static constexpr int value = F % 100;
+};
+
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
@@ -35,12 +47,13 @@ __device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t byte_off) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// A scale of SW bits (16: bf16 / fp16, 32: fp32), raw (converted only where it is used,
+// A scale of SW bits (8: E8M0, 16: bf16 / fp16, 32: fp32), raw (converted only where it is used,
 // so the load is not waited for early).
 template <int SW>
 __device__ __forceinline__ uint32_t buf_load_scale(rsrc_t r, uint32_t idx) {
   if constexpr (SW == 32) return __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4u, 0, 0);
-  else return __builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0);
+  else if constexpr (SW == 16) return __builtin_amdgcn_raw_buffer_load_b16(r, idx * 2u, 0, 0);
+  else return __builtin_amdgcn_raw_buffer_load_b8(r, idx, 0, 0);
 }
 
 // Raw scale bits of dtype `dt` (wave-uniform) as fp32; for 16-bit scales both readings are
@@ -49,6 +62,8 @@ template <int SW>
 __device__ __forceinline__ float scale_value(uint32_t b, int dt) {
   if constexpr (SW == 32) {
     return __builtin_bit_cast(float, b);
+  } else if constexpr (SW == 8) {
+    return e8m0_to_f32(b);
   } else {
     const float as_bf16 = __builtin_bit_cast(float, b << 16);
     const float as_fp16 = (float)__builtin_bit_cast(_Float16, (uint16_t)b);
@@ -60,10 +75,27 @@ __device__ __forceinline__ float scale_value(uint32_t b, int dt) {
 // activation dtype), accumulated into `acc`. Fast path: bf16/fp16 activations, 4- or
 // 8-bit codes.
 template <int BITS, int ACT>
-__device__ __forceinline__ float unit_dot_fast(const uint4& q, const uint32_t* xw, const GroupK& k,
+__device__ __forceinline__ float unit_dot_fast(const uint4& q, const uint32_t* xw, float s,
                                                const Masks& M, float acc) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  if constexpr (BITS == 4) {
+  if constexpr (BITS == F_E4M3) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wp[2];
+      deq_word_e4m3<ACT>(w[i], s, wp);
+      acc = dot2<ACT>(wp[0], xw[2 * i], acc);
+      acc = dot2<ACT>(wp[1], xw[2 * i + 1], acc);
+    }
+  } else if constexpr (BITS == F_MXFP4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wp[4];
+      deq_word_e2m1<ACT>(w[i], s, wp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = dot2<ACT>(wp[t], xw[4 * i + t], acc);
+    }
+  } else if constexpr (BITS == 4) {
+    const GroupK k = group_consts<4>(s);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wp[4];
@@ -72,6 +104,7 @@ __device__ __forceinline__ float unit_dot_fast(const uint4& q, const uint32_t* x
       for (int t = 0; t < 4; ++t) acc = dot2<ACT>(wp[t], xw[4 * i + t], acc);
     }
   } else {
+    const GroupK k = group_consts<8>(s);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wp[2];
@@ -87,14 +120,20 @@ __device__ __forceinline__ float unit_dot_fast(const uint4& q, const uint32_t* x
 template <int BITS, int ACT>
 __device__ __forceinline__ float unit_dot_general(const uint4& q, const uint32_t* xw,
                                                   float s_act, float acc) {
-  constexpr int PER = 32 / BITS;
+  constexpr int PER = 32 / CodeBits<BITS>::value;
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int jj = 0; jj < PER; ++jj) {
       const int e = i * PER + jj;
-      const float wt = deq_code<ACT, BITS>(w[i], jj, s_act);
+      float wt;
+      if constexpr (BITS == F_E4M3)
+        wt = round_act<ACT>(e4m3_to_f32((w[i] >> (8 * jj)) & 0xFFu) * s_act);
+      else if constexpr (BITS == F_MXFP4)
+        wt = round_act<ACT>(e2m1_to_f32((w[i] >> (4 * jj)) & 0xFu) * s_act);
+      else
+        wt = deq_code<ACT, BITS>(w[i], jj, s_act);
       float xval;
       if constexpr (ACT == DT_FP32) {
         xval = __builtin_bit_cast(float, xw[e]);
@@ -111,11 +150,11 @@ __device__ __forceinline__ float unit_dot_general(const uint4& q, const uint32_t
   return acc;
 }
 
-template <int BITS, int ACT>
+template <int F, int ACT>
 struct Unit {
-  static constexpr int CODES = 128 / BITS;                                  // per 16 B unit
+  static constexpr int CODES = 128 / CodeBits<F>::value;                    // per 16 B unit
   static constexpr int XD = (ACT == DT_FP32 ? 4 * CODES : 2 * CODES) / 4;   // x dwords
-  static constexpr bool FAST = ACT != DT_FP32 && (BITS == 4 || BITS == 8);
+  static constexpr bool FAST = ACT != DT_FP32 && (F == 4 || F == 8 || F >= 100);
 };
 
 // mask ? a : b bitwise; with an opaque all-ones / all-zeros mask one v_bfi_b32.
@@ -156,6 +195,7 @@ struct DecodeShape {
   int chunks;            // units per lane per row (CH) = units_row / lpr
   int groups_row;        // scales per row
   int ushift;            // log2(units per scale group)
+  int rshift;            // log2(rows per scale block): 0 but for block-scaled FP8
   int sc_dt;             // scale dtype code
   uint32_t role_bytes;   // bytes of one role's codes
   uint32_t role_scales;  // scales of one role
@@ -180,7 +220,7 @@ __device__ __forceinline__ void load_tile(RowTile<RI, CH>& t, rsrc_t codes, rsrc
   }
 #pragma unroll
   for (int r = 0; r < RI; ++r) {
-    const uint32_t sbase = (uint32_t)rows[r] * s.groups_row;
+    const uint32_t sbase = ((uint32_t)rows[r] >> s.rshift) * s.groups_row;
 #pragma unroll
     for (int c = 0; c < CH; ++c)
       t.s[r][c] = buf_load_scale<SW>(sc, sbase + ((j + c * s.lpr) >> s.ushift));
@@ -196,9 +236,10 @@ __device__ __forceinline__ void tile_dot(const RowTile<RI, CH>& t, const uint32_
     float a = acc[r * stride];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const float s_act = round_act<ACT>(scale_value<SW>(t.s[r][c], sc_dt));
+      const float sv = scale_value<SW>(t.s[r][c], sc_dt);
+      const float s_act = BITS >= 100 ? sv : round_act<ACT>(sv);
       if constexpr (UT::FAST) {
-        a = unit_dot_fast<BITS, ACT>(t.q[r][c], xw[c], group_consts<BITS>(s_act), M, a);
+        a = unit_dot_fast<BITS, ACT>(t.q[r][c], xw[c], s_act, M, a);
       } else {
         a = unit_dot_general<BITS, ACT>(t.q[r][c], xw[c], s_act, a);
       }
@@ -408,6 +449,14 @@ inline int ilog2(int v) {
 
 // Why the decode kernels cannot take this geometry, or nullptr.
 inline const char* decode_unsupported(const vaayu_geom* g, int act) {
+  if (g->format < 0 || g->format > 2) return "code format";
+  if (g->format == VAAYU_FMT_E4M3 && g->bits != 8) return "e4m3 codes are 8 bits";
+  if (g->format == VAAYU_FMT_MXFP4 && (g->bits != 4 || g->group != 32))
+    return "mxfp4 codes are 4 bits with one scale per 32";
+  if (g->format == VAAYU_FMT_E4M3 &&
+      (g->block_rows <= 0 || (g->block_rows & (g->block_rows - 1)) ||
+       g->hidden % g->block_rows || g->inter % g->block_rows))
+    return "e4m3 scale blocks must be a power of two rows dividing hidden and intermediate";
   if (g->bits != 1 && g->bits != 2 && g->bits != 4 && g->bits != 8) return "bit width";
   const int cpu = 128 / g->bits;                   // codes per 16-byte unit
   if (g->group % cpu || (g->group & (g->group - 1)))
@@ -426,6 +475,11 @@ struct Plan {
 };
 
 inline constexpr int kCH[] = {1, 2, 3, 4, 7};   // the instantiated chunks per lane
+
+// The kernels' code format F for a geometry (see Unit).
+inline int code_format(const vaayu_geom* g) {
+  return g->format == VAAYU_FMT_E4M3 ? F_E4M3 : g->format == VAAYU_FMT_MXFP4 ? F_MXFP4 : g->bits;
+}
 
 // Lanes per row LPR (a power of two in [min_lpr, 64]) and units per lane CH =
 // units_row / LPR from the instantiated set ({1, 2, 3, 4, 7} on the fast path, {1} on the
@@ -458,9 +512,10 @@ inline DecodeShape shape_for(const vaayu_geom* g, int n, int k_dim, int rows, in
   s.chunks = pl.ch;
   s.groups_row = k_dim / g->group;
   s.ushift = ilog2(g->group * g->bits / 128);
+  s.rshift = g->format == VAAYU_FMT_E4M3 ? ilog2(g->block_rows) : 0;
   s.sc_dt = sc_dt;
   s.role_bytes = (uint32_t)((int64_t)rows * k_dim * g->bits / 8);
-  s.role_scales = (uint32_t)((int64_t)rows * k_dim / g->group);
+  s.role_scales = (uint32_t)((int64_t)(rows >> s.rshift) * k_dim / g->group);
   return s;
 }
 

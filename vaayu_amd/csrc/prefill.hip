@@ -512,6 +512,7 @@ prefill_reduce_kernel(const float* __restrict__ y, const int64_t* __restrict__ o
 
 // Why the prefill kernels cannot take this geometry, or nullptr.
 const char* prefill_unsupported(const vaayu_geom* g, int act) {
+  if (g->format != VAAYU_FMT_INT) return "code format (the prefill kernels take packed integer codes)";
   if (act != DT_BF16 && act != DT_FP16) return "activation dtype (MFMA takes bf16 / fp16)";
   if (g->bits != 4 && g->bits != 8) return "bit width (the MFMA path takes 4 and 8)";
   const int cpu = 128 / g->bits;

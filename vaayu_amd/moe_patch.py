@@ -187,7 +187,11 @@ def build_expert_blob(by_role: dict) -> "dict | None":
 
 
 def dequantize_expert_blob(blob: dict, dtype: torch.dtype) -> dict:
-    """{role: dense weight} from a blob: one dequant over the flat stream, then views."""
+    """{role: dense weight} from a blob: one dequant over the flat stream, then views
+    (FP8 / MXFP4 blobs: their per-role dequant)."""
+    if isinstance(blob["geom"][0], str):
+        from .block_formats import dequantize_format_blob
+        return dequantize_format_blob(blob, dtype)
     bits, gs, roles = blob["geom"]
     packed, scale = blob["flat"]["packed"], blob["flat"]["scale"]
     flat = _fused_dequant_fn(bits, gs, dtype, packed.device.type)(packed, scale, bits, gs, dtype)

@@ -28,6 +28,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
+from .block_formats import blob_layout, geom_format, FMT_E4M3, FMT_MXFP4
 
 try:
     _lib.load()
@@ -48,6 +49,8 @@ _PF_BLOCK_M = 16
 _PF_MIN_TILE = 16
 _PF_GU_BK_MAX, _PF_DN_BK_MAX = 256, 256
 _DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+# Scale dtypes the kernels read: the activation dtypes, and E8M0 bytes (MXFP4 blobs).
+_SCALE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2, torch.uint8: 3}
 _ROLES = ("gate", "down", "up")
 
 
@@ -95,7 +98,10 @@ _PF_VERDICTS: dict = {}
 
 def _layout(geom) -> dict:
     """{role: (word offset, scale offset, rows, cols)} inside a blob's flat streams
-    (vaayu/packed_expert_kernels.py:301-309)."""
+    (vaayu/packed_expert_kernels.py:301-309); FP8 / MXFP4 blobs by their own scale blocking
+    (vaayu_amd.block_formats)."""
+    if isinstance(geom[0], str):
+        return blob_layout(geom)
     bits, gs, roles = geom
     out, w_at, s_at = {}, 0, 0
     for role, rows, cols in roles:
@@ -128,13 +134,15 @@ def _unsupported(geom, act_dtype, scale_dtype, w_dtype):
 
     The reference's rules (vaayu/packed_expert_kernels.py:329-346), plus what the HIP
     GEMV needs: a row is whole 16-byte units of codes, and a unit lies in one group."""
-    bits, gs, roles = geom
-    shapes = {r: (rows, cols) for r, rows, cols in roles}
+    shapes = {r: (rows, cols) for r, rows, cols in geom[2]}
     if set(shapes) != set(_ROLES):
         return f"expert roles {sorted(shapes)} are not gate/up/down"
     inter, hid = shapes["gate"]
     if shapes["up"] != (inter, hid) or shapes["down"] != (hid, inter):
         return f"projection shapes {shapes} are not a gated MLP"
+    if isinstance(geom[0], str):
+        return _format_unsupported(geom, act_dtype, scale_dtype, w_dtype, inter, hid)
+    bits, gs, roles = geom
     if gs & (gs - 1) or gs % (32 // bits):
         return f"group size {gs} is not a power of two holding whole {bits}-bit words"
     if _block_k(hid, gs) is None or _block_k(inter, gs) is None:
@@ -149,6 +157,31 @@ def _unsupported(geom, act_dtype, scale_dtype, w_dtype):
     if hid % (2 * unit) or inter % unit:
         return (f"hidden {hid} / intermediate {inter} is not whole (hidden: an even number "
                 f"of) 16-byte units of codes")
+    return None
+
+
+def _format_unsupported(geom, act_dtype, scale_dtype, w_dtype, inter, hid):
+    """Why the decode kernels cannot run an FP8 / MXFP4 blob, or None."""
+    try:
+        fmt, bits, group, brows = geom_format(geom)
+    except (TypeError, ValueError):
+        return f"code format {geom[0]!r}"
+    if fmt == FMT_E4M3:
+        if scale_dtype not in _DTYPE_CODE:
+            return f"e4m3 scale dtype {scale_dtype}"
+        if group & (group - 1) or group % 16 or brows & (brows - 1) or inter % brows or hid % brows:
+            return f"e4m3 scale blocks {brows} x {group} do not tile {inter} x {hid}"
+    elif fmt == FMT_MXFP4:
+        if scale_dtype != torch.uint8:
+            return f"mxfp4 scales are E8M0 bytes, not {scale_dtype}"
+    else:
+        return f"code format {geom[0]!r}"
+    for what, dt in (("activation", act_dtype), ("routing-weight", w_dtype)):
+        if dt not in _DTYPE_CODE:
+            return f"{what} dtype {dt}"
+    unit = 128 // bits
+    if hid % (2 * unit) or inter % unit or hid % group or inter % group:
+        return f"hidden {hid} / intermediate {inter} is not whole 16-byte units and scale groups"
     return None
 
 
@@ -198,7 +231,7 @@ def _launch(x, pairs, routing_weights, out) -> None:
     """The two decode kernels over `pairs`, into `out`. No checks: `_checked` gates this
     (vaayu/packed_expert_kernels.py:390-396)."""
     geom = pairs[0][0]["geom"]
-    sc = _DTYPE_CODE[pairs[0][0]["flat"]["scale"].dtype]
+    sc = _SCALE_CODE[pairs[0][0]["flat"]["scale"].dtype]
     tbl = _TABLES.put(_table_values(pairs), x.device)
     h = _gate_up(x, tbl, len(pairs), geom, sc)
     _down(h, tbl, routing_weights, out, len(pairs), geom, sc)
@@ -390,7 +423,7 @@ def _capture(layer, key, x, pairs, rw, shared, tail, vals, act_fn):
     """Record the layer's graph, replay it once and hold it bitwise to the eager launch
     (vaayu/packed_expert_kernels.py:578-654). Nothing here raises into the request."""
     geom = pairs[0][0]["geom"]
-    sc = _DTYPE_CODE[pairs[0][0]["flat"]["scale"].dtype]
+    sc = _SCALE_CODE[pairs[0][0]["flat"]["scale"].dtype]
     n = len(pairs)
     inter = _layout(geom)["gate"][2]
     dev = x.device
@@ -462,6 +495,8 @@ def _prefill_unsupported(geom, act_dtype, scale_dtype, w_dtype):
     """Why the grouped prefill kernels cannot run this geometry, or None
     (vaayu/packed_expert_kernels.py:657-673): the decode rules, no fp32 activations, and
     an MFMA K step -- 4 lanes' 16-byte units -- that divides hidden and intermediate."""
+    if isinstance(geom[0], str):
+        return f"code format {geom[0]!r} (the prefill kernels take packed integer codes)"
     why = _unsupported(geom, act_dtype, scale_dtype, w_dtype)
     if why is not None:
         return why
@@ -566,7 +601,7 @@ def _prefill_launch(x, eidx_cpu, routing_weights, blobs, out, plan=None) -> None
     strided `out` is written through a dense temporary."""
     plan = plan or _prefill_plan(eidx_cpu)
     blob = blobs[int(plan[1][0])]
-    geom, sc = blob["geom"], _DTYPE_CODE[blob["flat"]["scale"].dtype]
+    geom, sc = blob["geom"], _SCALE_CODE[blob["flat"]["scale"].dtype]
     top_k = eidx_cpu.shape[1]
     x = x.contiguous()
     tbl, rows, order, n_blocks = _prefill_tables(eidx_cpu, plan, blobs, x.device)
