@@ -144,6 +144,10 @@ def route(logits, top_k):
 # recorded in one HIP graph and replayed.
 WORKLOADS = {
     "qwen3-decode": None,      # the headline decode line (main)
+    "qwen3-fp8-decode": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, FP8 e4m3 "
+                                  "experts with fp32 scales per 128 x 128 block", fmt="e4m3"),
+    "qwen3-mxfp4-decode": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, MXFP4 "
+                                    "e2m1 experts with E8M0 scales per 32", fmt="mxfp4"),
     "dsv3-prefill": dict(name="DeepSeek-V3-shape MoE layer prefill, 2048 tokens", hidden=7168,
                          inter=2048, experts=256, top_k=8, tokens=2048, routing="zipf",
                          shared=True, bound="mfma"),
@@ -344,13 +348,16 @@ def main():
               "(expert-parallel sharding is a design note only). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload != "qwen3-decode":
-        bench_prefill(args, WORKLOADS[args.workload])
+    spec = WORKLOADS[args.workload]
+    if spec is not None and "fmt" not in spec:
+        bench_prefill(args, spec)
         return
+    fmt = spec["fmt"] if spec is not None else "int4"
 
     import vaayu_amd.packed_expert_kernels as pk
     from vaayu_amd import _lib
     from vaayu_amd.synth import clone_blob, random_expert
+    from vaayu_amd.block_formats import random_format_expert
 
     if pk.triton is None:
         raise SystemExit("vaayu_amd kernel library missing: run `python -m vaayu_amd.build`")
@@ -363,9 +370,12 @@ def main():
     # ── experts: `distinct` random layers, the rest byte copies at fresh addresses ─────
     t0 = time.time()
     gen = torch.Generator(device=dev).manual_seed(1234)
-    base = [[random_expert(H, I, BITS, GS, generator=gen, device=dev, std=0.02,
-                           scale_dtype=torch.float16) for _ in range(E)]
-            for _ in range(min(args.distinct, L))]
+    if fmt == "int4":
+        make = lambda: random_expert(H, I, BITS, GS, generator=gen, device=dev, std=0.02,
+                                     scale_dtype=torch.float16)
+    else:
+        make = lambda: random_format_expert(fmt, H, I, generator=gen, device=dev, std=0.02)
+    base = [[make() for _ in range(E)] for _ in range(min(args.distinct, L))]
     layers = [base[l] if l < len(base) else [clone_blob(b) for b in base[l % len(base)]]
               for l in range(L)]
     torch.cuda.synchronize()
@@ -373,7 +383,7 @@ def main():
     log(f"{L} layers x {E} experts resident: {L * E * per_expert / 1e9:.2f} GB "
         f"({time.time() - t0:.1f} s)")
     geom = layers[0][0]["geom"]
-    sc = pk._DTYPE_CODE[torch.float16]
+    sc = pk._SCALE_CODE[layers[0][0]["flat"]["scale"].dtype]
     g = _lib.geom_struct(geom)
 
     # ── one token's routing per layer, its table and buffers ────────────────────────────
@@ -449,9 +459,15 @@ def main():
         f"{ms_gu * 1000 / L:.2f} us, down {ms_dn * 1000 / L:.2f} us per launch")
 
     # algorithmic bytes (distinct routed experts' codes + scales + activations)
-    sc_bytes = 2
-    gu_bytes = K * (2 * I * H * BITS // 8 + 2 * (I * H // GS) * sc_bytes) + H * 2 + K * I * 2
-    dn_bytes = K * (H * I * BITS // 8 + (H * I // GS) * sc_bytes) + K * I * 2 + H * 4
+    from vaayu_amd.block_formats import geom_format
+    _f, bits, group, brows = geom_format(geom)
+    sc_el = layers[0][0]["flat"]["scale"].element_size()
+
+    def role_bytes(rows, cols):             # codes + scales of one role
+        return rows * cols * bits // 8 + (rows // brows) * (cols // group) * sc_el
+
+    gu_bytes = K * 2 * role_bytes(I, H) + H * 2 + K * I * 2
+    dn_bytes = K * role_bytes(H, I) + K * I * 2 + H * 4
     gu_gbs = gu_bytes / (ms_gu * 1e-3 / L) / 1e9
     dn_gbs = dn_bytes / (ms_dn * 1e-3 / L) / 1e9
     layer_gbs = (gu_bytes + dn_bytes) / (us_tok_layer * 1e-6) / 1e9
@@ -498,15 +514,17 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"Qwen3-30B-A3B-shape MoE layer decode, 1 token, int4 g128 "
-                               f"fp16 scales, {L} HBM-resident layers per step",
+        "config": {"workload": (spec["name"] if spec is not None else
+                                "Qwen3-30B-A3B-shape MoE layer decode, 1 token, int4 g128 fp16 "
+                                "scales") + f", {L} HBM-resident layers per step",
                    "hidden": H, "experts": E, "inter": I, "top_k": K, "layers": L,
                    "tokens": 1, "parallelism": "none (one GPU)"},
         "tokens_per_s_per_layer": round(1e6 / us_tok_layer, 1),
         "layer_hbm_gbs": round(layer_gbs, 1),
         "roofline": {"bound": "hbm", "kernel": "decode_gate_up_kernel",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profile() if fmt == "int4" else None,
                      "bytes_per_launch": gu_bytes,
                      "us_per_launch": round(ms_gu * 1000 / L, 3)},
         "down_kernel": {"achieved_gbs": round(dn_gbs, 1), "bytes_per_launch": dn_bytes,

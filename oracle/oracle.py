@@ -536,8 +536,39 @@ def upcast_mx_e4m3(codes_u8, scale_e8m0, act="bf16") -> np.ndarray:
 
 # ── the CPU baseline: the stock loop itself on torch CPU ─────────────────────────────────
 
+def _dequant_format_torch(blob, dtype):
+    """FP8 / MXFP4 blob roles on torch CPU, as the reference's dequant functions compute
+    them (vaayu/model_code/deepseek_v4/modeling_deepseek_v4.py:228-240; vendor
+    …/numerics_details/mxfp.py:238-299)."""
+    kind, gs, roles = blob["geom"]
+    codes = blob["flat"]["packed"].contiguous().view(torch.uint8)
+    scale = blob["flat"]["scale"]
+    out, c_at, s_at = {}, 0, 0
+    for role, rows, cols in roles:
+        if kind == "e4m3":
+            bo, bi = gs
+            n_c, n_s = rows * cols, (rows // bo) * (cols // bi)
+            w = codes[c_at:c_at + n_c].view(torch.float8_e4m3fn).view(rows, cols)
+            sc = scale[s_at:s_at + n_s].view(rows // bo, cols // bi)
+            t = w.unflatten(0, (-1, bo)).unflatten(-1, (-1, bi)).float() * sc[:, None, :, None].float()
+            out[role] = t.flatten(2, 3).flatten(0, 1).to(dtype)
+        else:
+            n_c, n_s = rows * cols // 2, rows * cols // 32
+            q = codes[c_at:c_at + n_c].view(rows, cols // 2).to(torch.int32)
+            lut = torch.tensor(E2M1 + tuple(-v for v in E2M1), dtype=torch.float32)
+            vals = torch.stack([lut[q & 0xF], lut[(q >> 4) & 0xF]], -1).view(rows, cols)
+            s8 = scale[s_at:s_at + n_s].view(rows, cols // 32).to(torch.int32)
+            f = torch.where(s8 == 0xFF, torch.tensor(float("nan")), (s8 << 23).view(torch.float32))
+            out[role] = (vals * f.repeat_interleave(32, dim=-1)).to(dtype)
+        c_at += n_c
+        s_at += n_s
+    return out["gate"], out["down"], out["up"]
+
+
 def _dequant_torch(blob, dtype):
     """`_fused_dequant_kernel` eager on torch CPU (vaayu/moe_patch.py:750-769)."""
+    if isinstance(blob["geom"][0], str):
+        return _dequant_format_torch(blob, dtype)
     bits, gs, roles = blob["geom"]
     packed, scale = blob["flat"]["packed"], blob["flat"]["scale"]
     per = 32 // bits

@@ -240,22 +240,50 @@ __device__ __forceinline__ uint32_t pack_act(float a, float b) {
 }
 
 // e4m3 word (4 codes, code k in byte k) -> 2 packed weight pairs round_act(fp32(c) * s):
-// the fp32 product rounded once, then one rounding to the activation dtype.
+// the fp32 product rounded once, then one rounding to the activation dtype. The codes are
+// widened by v_cvt_pk_f32_fp8 (gfx950: OCP e4m3fn, exact for all 256 codes, NaN kept).
 template <int ACT>
 __device__ __forceinline__ void deq_word_e4m3(uint32_t w, float s, uint32_t out[2]) {
-  const float f0 = e4m3_to_f32(w & 0xFFu) * s, f1 = e4m3_to_f32((w >> 8) & 0xFFu) * s;
-  const float f2 = e4m3_to_f32((w >> 16) & 0xFFu) * s, f3 = e4m3_to_f32(w >> 24) * s;
-  out[0] = pack_act<ACT>(f0, f1);
-  out[1] = pack_act<ACT>(f2, f3);
+#if defined(__HIP_DEVICE_COMPILE__)        // gfx950 instructions: no host-pass form
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  out[0] = pack_act<ACT>(lo.x * s, lo.y * s);
+  out[1] = pack_act<ACT>(hi.x * s, hi.y * s);
+#else
+  out[0] = out[1] = w;
+  (void)s;
+#endif
 }
 
-// e2m1 word (8 codes, code k in bits 4k..4k+3) -> 4 packed weight pairs round_act(e2m1 * s).
+// e2m1 word (8 codes, code k in bits 4k..4k+3) -> 4 packed weight pairs round_act(e2m1 * s),
+// s the E8M0 scale as fp32 (2^(e-127); 0 for e = 0; NaN for e = 255). The products are exact
+// (e2m1 has two significant bits, s is a power of two). v_cvt_scalef32_pk_*_fp4 applies the
+// scale by its exponent field, which gives 2^-127 rather than 0 for s = 0: there the codes'
+// magnitude bits are cleared first (signs kept), so every product is the reference's +-0.
 template <int ACT>
 __device__ __forceinline__ void deq_word_e2m1(uint32_t w, float s, uint32_t out[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    out[k] = pack_act<ACT>(e2m1_to_f32((w >> (8 * k)) & 0xFu) * s,
-                           e2m1_to_f32((w >> (8 * k + 4)) & 0xFu) * s);
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t keep = __builtin_bit_cast(uint32_t, s) == 0 ? 0x88888888u : 0xFFFFFFFFu;
+  const uint32_t c = w & keep;
+  if constexpr (ACT == DT_BF16) {
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, s, 0));
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, s, 1));
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, s, 2));
+    out[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, s, 3));
+  } else {
+    const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, s, 0);
+    const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, s, 1);
+    const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, s, 2);
+    const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, s, 3);
+    out[0] = pack_act<ACT>(v0.x, v0.y);
+    out[1] = pack_act<ACT>(v1.x, v1.y);
+    out[2] = pack_act<ACT>(v2.x, v2.y);
+    out[3] = pack_act<ACT>(v3.x, v3.y);
+  }
+#else
+  out[0] = out[1] = out[2] = out[3] = w;
+  (void)s;
+#endif
 }
 
 // ── wavefront reductions ───────────────────────────────────────────────────────────────
