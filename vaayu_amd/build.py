@@ -20,6 +20,9 @@ CFLAGS = [
     "-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 16 dwords of kernel arguments arrive in SGPRs (the table and vector
+    # pointers lead the decode kernels' arguments, so their loads issue at once)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -1,7 +1,82 @@
-// Decode down entry: vaayu_decode_down (kernels in decode_kernels.hpp).
-#include "decode_kernels.hpp"
+// Decode down entry: vaayu_decode_down (kernels in decode_mfma.hpp for bf16 / fp16
+// activations with 4- and 8-bit codes, decode_kernels.hpp otherwise).
+#include "decode_mfma.hpp"
 
 namespace vaayu {
+
+struct DownPlan {
+  MShape s;
+  int kp, ps, nrg;
+  size_t lds;
+  unsigned blocks;
+};
+
+// Step counts with a straight-line kernel; others run the chunked loop (NS = 0).
+template <int F, int ACT, int SW>
+static int mfma_down_at(const void* h, const int64_t* tbl, const void* rw, int rw_dt, float* out,
+                        const DownPlan& d, int w_round, hipStream_t st) {
+  const int kps = d.kp == 4 ? 2 : d.kp == 2 ? 1 : 0;
+#define DN(NS_) hipLaunchKernelGGL((mfma_down_kernel<F, ACT, SW, NS_>), dim3(d.blocks), dim3(512), \
+                                   d.lds, st, tbl, h, rw, out, d.s, rw_dt, kps, d.ps, d.nrg,      \
+                                   w_round)
+  switch (d.s.steps) {
+    case 1: DN(1); break;
+    case 2: DN(2); break;
+    case 3: DN(3); break;
+    case 4: DN(4); break;
+    case 8: DN(8); break;
+    default: DN(0); break;
+  }
+#undef DN
+  return 0;
+}
+
+template <int F, int ACT>
+static int mfma_down_sw(const void* h, const int64_t* tbl, const void* rw, int rw_dt, float* out,
+                        const DownPlan& d, int sc, int w_round, hipStream_t st) {
+  if constexpr (F == F_MXFP4) {
+    if (sc == VAAYU_E8M0) return mfma_down_at<F, ACT, 8>(h, tbl, rw, rw_dt, out, d, w_round, st);
+    return set_error(-2, "mxfp4 scales are E8M0");
+  } else {
+    if (sc == VAAYU_E8M0) return set_error(-2, "E8M0 scales go with mxfp4 codes");
+    if (sc == DT_FP32) return mfma_down_at<F, ACT, 32>(h, tbl, rw, rw_dt, out, d, w_round, st);
+    return mfma_down_at<F, ACT, 16>(h, tbl, rw, rw_dt, out, d, w_round, st);
+  }
+}
+
+// The MFMA kernel's plan for this launch, or false when it does not take it. K parts: the
+// most of 4, 2, 1 that split the intermediate dimension into whole steps (4 units each).
+// Row groups per wave (nrg) keep the grid near 512 blocks at most, since every block stages
+// all pairs' h.
+static bool mfma_down_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, DownPlan& d) {
+  if (!mfma_format(fmt, act)) return false;
+  const int cpu = 128 / (fmt % 100);
+  if (g->inter % cpu) return false;
+  const int units = g->inter / cpu;
+  d.kp = units % 16 == 0 ? 4 : units % 8 == 0 ? 2 : units % 4 == 0 ? 1 : 0;
+  if (!d.kp) return false;
+  d.s = mfma_shape(g, fmt, n, g->hidden, g->inter, d.kp, sc);
+  const int64_t vec16 = (int64_t)n * g->inter / 8;
+  if (vec16 > 8 * 512) return false;                          // h: up to 8 uint4 per thread
+  d.s.vec16 = (int)vec16;
+  d.ps = 1;
+  while (d.ps < 8 && d.ps < n) d.ps <<= 1;
+  const int rows_g = (8 / d.ps) * (16 / d.kp);               // rows per block per row group
+  const int64_t blocks1 = (g->hidden + rows_g - 1) / rows_g;
+  d.nrg = (int)std::max<int64_t>(1, (blocks1 + 511) / 512);
+  const int br = d.nrg * rows_g;
+  d.blocks = (unsigned)((g->hidden + br - 1) / br);
+  d.lds = (size_t)vec16 * 16 + (size_t)n * br * sizeof(float);
+  if (d.lds > 64 * 1024) return false;
+  const int64_t role_bytes = (int64_t)g->hidden * g->inter * g->bits / 8;
+  const int64_t role_scales = (int64_t)(g->hidden >> d.s.rshift) * (g->inter / g->group);
+  if (role_bytes > 0xFFFFFFFFll || role_scales * scale_bytes_of(sc) > 0xFFFFFFFFll) return false;
+  d.s.wb0 = (uint32_t)(g->down_w * 4);
+  d.s.sc0 = (uint32_t)g->down_s;
+  d.s.code_bytes = (uint32_t)role_bytes;
+  d.s.scale_bytes = (uint32_t)(role_scales * scale_bytes_of(sc));
+  return true;
+}
 
 template <int BITS, int ACT, int SW, int CH>
 static int down_at(const void* h, const int64_t* tbl, const void* rw, int rw_dt, float* out,
@@ -78,11 +153,23 @@ extern "C" int vaayu_decode_down(const void* h, const int64_t* table, const void
   if (((uintptr_t)h) & 15) return set_error(-1, "h must be 16-byte aligned");
   if (const char* why = decode_unsupported(geom, act)) return set_error(-2, why);
   const int fmt = code_format(geom);
+  hipStream_t st = (hipStream_t)stream;
+  {
+    DownPlan d;
+    if (mfma_down_plan(geom, fmt, act, n_pairs, scale_dtype, d)) {
+      int rc;
+#define BA(B_, A_) else if (fmt == B_ && act == A_) rc = mfma_down_sw<B_, A_>(h, table, routing_weights, rw_dtype, out, d, scale_dtype, w_round, st);
+      if (false) rc = 0;
+      BA(4, 0) BA(4, 1) BA(8, 0) BA(8, 1) BA(F_E4M3, 0) BA(F_E4M3, 1) BA(F_MXFP4, 0) BA(F_MXFP4, 1)
+      else rc = set_error(-2, "unsupported code format / activation dtype");
+#undef BA
+      return rc ? rc : check_launch("decode down");
+    }
+  }
   const bool fast = (fmt == 4 || fmt == 8 || fmt >= 100) && act != DT_FP32;
   const Plan pl = plan_row(geom->inter * geom->bits / 128, 1, 1, fast);
   if (pl.lpr == 0) return set_error(-2, "decode down: no lane split of this row is built");
   const DecodeShape s = shape_for(geom, n_pairs, geom->inter, geom->hidden, scale_dtype, pl);
-  hipStream_t st = (hipStream_t)stream;
   int rc;
 #define BA(B_, A_) else if (fmt == B_ && act == A_) rc = by_sw<B_, A_>(h, table, routing_weights, rw_dtype, out, s, geom, scale_dtype, w_round, st);
   if (false) rc = 0;

@@ -1,7 +1,67 @@
-// Decode gate/up entry: vaayu_decode_gate_up (kernels in decode_kernels.hpp).
-#include "decode_kernels.hpp"
+// Decode gate/up entry: vaayu_decode_gate_up (kernels in decode_mfma.hpp for bf16 / fp16
+// activations with 4- and 8-bit codes, decode_kernels.hpp otherwise).
+#include "decode_mfma.hpp"
 
 namespace vaayu {
+
+// Step counts with a straight-line kernel; others run the chunked loop (NS = 0).
+template <int F, int ACT, int SW>
+static int mfma_gate_up_at(const void* x, const int64_t* tbl, void* h, const MShape& s, int xs,
+                           hipStream_t st) {
+  const dim3 grid((unsigned)((s.rows + 7) / 8), (unsigned)s.n_pairs), block(256);
+  const size_t lds = (size_t)xs * 256 * 16;
+#define GU(NS_) hipLaunchKernelGGL((mfma_gate_up_kernel<F, ACT, SW, NS_>), grid, block, lds, st, \
+                                   tbl, (const uint32_t*)x, h, s)
+  switch (s.steps) {
+    case 1: GU(1); break;
+    case 2: GU(2); break;
+    case 3: GU(3); break;
+    case 4: GU(4); break;
+    case 8: GU(8); break;
+    default: GU(0); break;
+  }
+#undef GU
+  return 0;
+}
+
+template <int F, int ACT>
+static int mfma_gate_up_sw(const void* x, const int64_t* tbl, void* h, const MShape& s, int xs,
+                           int sc, hipStream_t st) {
+  if constexpr (F == F_MXFP4) {
+    if (sc == VAAYU_E8M0) return mfma_gate_up_at<F, ACT, 8>(x, tbl, h, s, xs, st);
+    return set_error(-2, "mxfp4 scales are E8M0");
+  } else {
+    if (sc == VAAYU_E8M0) return set_error(-2, "E8M0 scales go with mxfp4 codes");
+    if (sc == DT_FP32) return mfma_gate_up_at<F, ACT, 32>(x, tbl, h, s, xs, st);
+    return mfma_gate_up_at<F, ACT, 16>(x, tbl, h, s, xs, st);
+  }
+}
+
+// The MFMA kernel's shape for this launch, or false when it does not take it: hidden is a
+// multiple of 16 units (4 K parts x 4 lane quarters), x fits 4 uint4 per thread, and the
+// two roles lie within 4 GiB of the blob's packed address.
+static bool mfma_gate_up_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, MShape& s,
+                              int& xs) {
+  if (!mfma_format(fmt, act)) return false;
+  const int cpu = 128 / (fmt % 100);
+  if (g->hidden % cpu || (g->hidden / cpu) % 16) return false;
+  s = mfma_shape(g, fmt, n, g->inter, g->hidden, 4, sc);
+  s.vec16 = g->hidden / 8;
+  xs = (s.vec16 + 255) / 256;
+  if (xs > 4) return false;
+  const int64_t role_bytes = (int64_t)g->inter * g->hidden * g->bits / 8;
+  const int64_t code_end = std::max(g->gate_w, g->up_w) * 4 + role_bytes;
+  const int64_t role_scales = (int64_t)(g->inter >> s.rshift) * (g->hidden / g->group);
+  const int64_t scale_end = (std::max(g->gate_s, g->up_s) + role_scales) * scale_bytes_of(sc);
+  if (code_end > 0xFFFFFFFFll || scale_end > 0xFFFFFFFFll) return false;
+  s.wb0 = (uint32_t)(g->gate_w * 4);
+  s.wb1 = (uint32_t)(g->up_w * 4);
+  s.sc0 = (uint32_t)g->gate_s;
+  s.sc1 = (uint32_t)g->up_s;
+  s.code_bytes = (uint32_t)code_end;
+  s.scale_bytes = (uint32_t)scale_end;
+  return true;
+}
 
 // Fast path: 4/8-bit codes with bf16/fp16 activations, any CH of the instantiated set.
 // General path (fp32 activations, 1/2-bit codes): CH = 1.
@@ -61,11 +121,24 @@ extern "C" int vaayu_decode_gate_up(const void* x, const int64_t* table, void* h
   if (((uintptr_t)x) & 15) return set_error(-1, "x must be 16-byte aligned");
   if (const char* why = decode_unsupported(geom, act)) return set_error(-2, why);
   const int fmt = code_format(geom);
+  hipStream_t st = (hipStream_t)stream;
+  {
+    MShape ms;
+    int xs;
+    if (mfma_gate_up_plan(geom, fmt, act, n_pairs, scale_dtype, ms, xs)) {
+      int rc;
+#define BA(B_, A_) else if (fmt == B_ && act == A_) rc = mfma_gate_up_sw<B_, A_>(x, table, h, ms, xs, scale_dtype, st);
+      if (false) rc = 0;
+      BA(4, 0) BA(4, 1) BA(8, 0) BA(8, 1) BA(F_E4M3, 0) BA(F_E4M3, 1) BA(F_MXFP4, 0) BA(F_MXFP4, 1)
+      else rc = set_error(-2, "unsupported code format / activation dtype");
+#undef BA
+      return rc ? rc : check_launch("decode gate/up");
+    }
+  }
   const bool fast = (fmt == 4 || fmt == 8 || fmt >= 100) && act != DT_FP32;
   const Plan pl = plan_row(geom->hidden * geom->bits / 128, 2, 2, fast);
   if (pl.lpr == 0) return set_error(-2, "decode gate/up: no lane split of this row is built");
   const DecodeShape s = shape_for(geom, n_pairs, geom->hidden, geom->inter, scale_dtype, pl);
-  hipStream_t st = (hipStream_t)stream;
   int rc;
 #define BA(B_, A_) else if (fmt == B_ && act == A_) rc = by_sw<B_, A_>(x, table, h, s, geom, scale_dtype, st);
   if (false) rc = 0;
