@@ -57,6 +57,7 @@ def parse():
 # calibration dispatch), which turns the counters into HBM bytes.
 CALIB_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_qwen3_b1_traffic.txt")
+GU_KERNEL = "mfma_gate_up_kernel"     # the decode gate/up kernel bf16 activations run
 
 
 def _csv_rows(d, suffix):
@@ -107,8 +108,8 @@ def summarize(dirs):
             avg = sum(vals) / len(vals)
             scaled = avg * 1024.0 * factors.get(ctr, 1.0)
             out.append(f"{name:<90} {ctr:>10} {len(vals):>10} {avg:>12.1f} {scaled:>14.0f}")
-            if "decode_gate_up_kernel" in name:
-                out.append(f"traffic_bytes decode_gate_up_kernel {ctr} {scaled:.0f}")
+            if GU_KERNEL in name:
+                out.append(f"traffic_bytes {GU_KERNEL} {ctr} {scaled:.0f}")
     return "\n".join(out)
 
 
@@ -120,7 +121,7 @@ def traffic_from_profile():
     total, seen = 0.0, set()
     for line in open(TRAFFIC_FILE):
         f = line.split()
-        if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == "decode_gate_up_kernel":
+        if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == GU_KERNEL:
             total += float(f[3])
             seen.add(f[2])
     return round(total) if seen == {"FETCH_SIZE", "WRITE_SIZE"} else None
@@ -521,7 +522,7 @@ def main():
                    "tokens": 1, "parallelism": "none (one GPU)"},
         "tokens_per_s_per_layer": round(1e6 / us_tok_layer, 1),
         "layer_hbm_gbs": round(layer_gbs, 1),
-        "roofline": {"bound": "hbm", "kernel": "decode_gate_up_kernel",
+        "roofline": {"bound": "hbm", "kernel": GU_KERNEL,
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile() if fmt == "int4" else None,
