@@ -158,6 +158,17 @@ WORKLOADS = {
     "qwen3-decode-b8": dict(name="Qwen3-30B-A3B-shape MoE layer decode, batch of 8 tokens",
                             hidden=2048, inter=768, experts=128, top_k=8, tokens=8,
                             routing="softmax", shared=False, bound="hbm"),
+    "qwen3-prefill": dict(name="Qwen3-30B-A3B-shape MoE layer prefill, 256 tokens", hidden=2048,
+                          inter=768, experts=128, top_k=8, tokens=256, routing="softmax",
+                          shared=False, bound="hbm"),
+    "qwen3-fp8-prefill": dict(name="Qwen3-30B-A3B-shape MoE layer prefill, 256 tokens, FP8 e4m3 "
+                                   "experts with fp32 scales per 128 x 128 block", hidden=2048,
+                              inter=768, experts=128, top_k=8, tokens=256, routing="softmax",
+                              shared=False, bound="hbm", fmt="e4m3"),
+    "qwen3-mxfp4-prefill": dict(name="Qwen3-30B-A3B-shape MoE layer prefill, 256 tokens, MXFP4 "
+                                     "e2m1 experts with E8M0 scales per 32", hidden=2048,
+                                inter=768, experts=128, top_k=8, tokens=256, routing="softmax",
+                                shared=False, bound="hbm", fmt="mxfp4"),
 }
 MFMA_PEAK_TFLOPS = 2500.0
 
@@ -187,8 +198,14 @@ def bench_prefill(args, spec):
     t0 = time.time()
     gen = torch.Generator(device=dev).manual_seed(1234)
     n_exp = E + (1 if spec["shared"] else 0)
-    blobs = {e: random_expert(H, I, BITS, GS, generator=gen, device=dev, std=0.02,
-                              scale_dtype=torch.float16) for e in range(n_exp)}
+    fmt = spec.get("fmt")
+    if fmt is None:
+        blobs = {e: random_expert(H, I, BITS, GS, generator=gen, device=dev, std=0.02,
+                                  scale_dtype=torch.float16) for e in range(n_exp)}
+    else:
+        from vaayu_amd.block_formats import random_format_expert
+        blobs = {e: random_format_expert(fmt, H, I, generator=gen, device=dev, std=0.02)
+                 for e in range(n_exp)}
     torch.cuda.synchronize()
     per_expert = sum(t.numel() * t.element_size() for t in blobs[0]["flat"].values())
     log(f"{n_exp} experts resident: {n_exp * per_expert / 1e9:.2f} GB ({time.time() - t0:.1f} s)")
@@ -200,7 +217,7 @@ def bench_prefill(args, spec):
         w, eidx = route(torch.randn(T, E, generator=cg), K)
     w = w.to(dev)
     geom = blobs[0]["geom"]
-    sc = pk._DTYPE_CODE[torch.float16]
+    sc = pk._SCALE_CODE[blobs[0]["flat"]["scale"].dtype]
 
     # calls of this layer: the routed experts, then (DeepSeek) the shared expert as a
     # one-slot call over every token with weight 1, added after the routed sum is cast
@@ -327,7 +344,8 @@ def bench_prefill(args, spec):
         "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": spec["name"] + ", int4 g128 fp16 scales", "hidden": H,
+        "config": {"workload": spec["name"] + ("" if fmt else ", int4 g128 fp16 scales"),
+                   "hidden": H,
                    "experts": E, "inter": I, "top_k": K, "tokens": T,
                    "shared_expert": spec["shared"], "routing": spec["routing"],
                    "parallelism": "none (one GPU)"},
@@ -350,7 +368,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     spec = WORKLOADS[args.workload]
-    if spec is not None and "fmt" not in spec:
+    if spec is not None and "tokens" in spec:
         bench_prefill(args, spec)
         return
     fmt = spec["fmt"] if spec is not None else "int4"

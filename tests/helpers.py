@@ -70,12 +70,12 @@ def frac_equal(a, b):
 
 
 @functools.lru_cache(maxsize=None)
-def format_blobs(fmt, hid, inter, k, device="cuda"):
+def format_blobs(fmt, hid, inter, k, device="cuda", std=0.05):
     """k distinct FP8 ("e4m3", 128 x 128 fp32 block scales) or MXFP4 ("mxfp4", E8M0 per 32)
-    expert blobs of N(0, 0.05) weights, built on the CPU and copied to `device`."""
+    expert blobs of N(0, std) weights, built on the CPU and copied to `device`."""
     from vaayu_amd.block_formats import random_format_expert
     g = torch.Generator().manual_seed(hid * 3 + inter + len(fmt))
-    blobs = [random_format_expert(fmt, hid, inter, generator=g, device="cpu", std=0.05)
+    blobs = [random_format_expert(fmt, hid, inter, generator=g, device="cpu", std=std)
              for _ in range(k)]
     return tuple(to_device(b, device) for b in blobs)
 

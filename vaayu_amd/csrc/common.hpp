@@ -286,6 +286,60 @@ __device__ __forceinline__ void deq_word_e2m1(uint32_t w, float s, uint32_t out[
 #endif
 }
 
+// ── code formats ────────────────────────────────────────────────────────────────────────
+//
+// Code formats F of the kernels: 1, 2, 4, 8 are packed unsigned integers of that many bits
+// (offset 2^(F-1), scale rounded to the activation dtype); F_E4M3 is float8 e4m3fn with fp32
+// block scales, F_MXFP4 is e2m1 with an E8M0 scale per 32 codes (both scales applied
+// unrounded, as the reference's dequant does).
+enum { F_MXFP4 = 104, F_E4M3 = 108 };
+
+template <int F>
+struct CodeBits {
+  static constexpr int value = F % 100;
+};
+
+// A unit's scale as the weights take it: rounded to the activation dtype for integer codes,
+// as is for e4m3 and e2m1.
+template <int F, int ACT>
+__device__ __forceinline__ float applied_scale(float s) {
+  if constexpr (F < 100) return round_act<ACT>(s);
+  else return s;
+}
+
+// MFMA operand i (8 weights as 4 packed pairs of the activation dtype, in code order) of one
+// 16-byte unit of codes of format F (bf16 / fp16 activations): word i of 4-bit codes, words
+// 2i and 2i+1 of 8-bit codes. k: the group constants of the applied scale (integer codes);
+// s: the applied scale (e4m3, e2m1).
+template <int F, int ACT>
+__device__ __forceinline__ uint4 operand_i(const uint4& q, const GroupK& k, float s,
+                                           const Masks& M, int i) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (F == 4 || F == F_MXFP4) {
+    uint32_t p[4];
+    if constexpr (F == 4) deq_word_i4<ACT>(w[i], k, M, p);
+    else deq_word_e2m1<ACT>(w[i], s, p);
+    return make_uint4(p[0], p[1], p[2], p[3]);
+  } else {
+    uint32_t p0[2], p1[2];
+    if constexpr (F == 8) {
+      deq_word_i8<ACT>(w[2 * i], k, M, p0);
+      deq_word_i8<ACT>(w[2 * i + 1], k, M, p1);
+    } else {
+      deq_word_e4m3<ACT>(w[2 * i], s, p0);
+      deq_word_e4m3<ACT>(w[2 * i + 1], s, p1);
+    }
+    return make_uint4(p0[0], p0[1], p1[0], p1[1]);
+  }
+}
+
+// Group constants for a unit of format F (zero for e4m3 / e2m1, which do not use them).
+template <int F>
+__device__ __forceinline__ GroupK group_of(float s_applied) {
+  if constexpr (F == 4 || F == 8) return group_consts<F>(s_applied);
+  else return GroupK{};
+}
+
 // ── wavefront reductions ───────────────────────────────────────────────────────────────
 
 template <int WIDTH>

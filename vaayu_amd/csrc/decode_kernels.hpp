@@ -25,17 +25,6 @@ namespace vaayu {
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-// Code formats F of the decode kernels: 1, 2, 4, 8 are packed unsigned integers of that
-// many bits (offset 2^(F-1), scale rounded to the activation dtype); F_E4M3 is float8
-// e4m3fn with fp32 block scales, F_MXFP4 is e2m1 with an E8M0 scale per 32 codes (both
-// scales applied unrounded, as the reference's dequant does).
-enum { F_MXFP4 = 104, F_E4M3 = 108 };
-
-template <int F>
-struct CodeBits {
-  static constexpr int value = F % 100;
-};
-
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,

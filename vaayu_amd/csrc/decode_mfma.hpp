@@ -45,38 +45,14 @@ struct MUnit {
 };
 
 // The B operands of one unit of codes: NMF uint4 of 8 weights (4 packed pairs) each, in code
-// order. `s` is the scale as it is applied: rounded to the activation dtype for integer
-// codes, raw (fp32 / E8M0 value) for e4m3 and e2m1.
+// order. `s` is the applied scale (rounded to the activation dtype for integer codes, raw
+// fp32 / E8M0 value for e4m3 and e2m1).
 template <int F, int ACT>
 __device__ __forceinline__ void unit_b(const uint4& q, float s, const Masks& M,
                                        uint4 (&b)[MUnit<F>::NMF]) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  if constexpr (F == 4 || F == F_MXFP4) {
-    GroupK k{};
-    if constexpr (F == 4) k = group_consts<4>(s);
+  const GroupK k = group_of<F>(s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t p[4];
-      if constexpr (F == 4) deq_word_i4<ACT>(w[i], k, M, p);
-      else deq_word_e2m1<ACT>(w[i], s, p);
-      b[i] = make_uint4(p[0], p[1], p[2], p[3]);
-    }
-  } else {
-    GroupK k{};
-    if constexpr (F == 8) k = group_consts<8>(s);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t p0[2], p1[2];
-      if constexpr (F == 8) {
-        deq_word_i8<ACT>(w[2 * i], k, M, p0);
-        deq_word_i8<ACT>(w[2 * i + 1], k, M, p1);
-      } else {
-        deq_word_e4m3<ACT>(w[2 * i], s, p0);
-        deq_word_e4m3<ACT>(w[2 * i + 1], s, p1);
-      }
-      b[i] = make_uint4(p0[0], p0[1], p1[0], p1[1]);
-    }
-  }
+  for (int i = 0; i < MUnit<F>::NMF; ++i) b[i] = operand_i<F, ACT>(q, k, s, M, i);
 }
 
 // One MFMA decode launch's geometry (filled on the host by mfma_shape).
@@ -133,8 +109,7 @@ struct ColumnDot {
 
   __device__ __forceinline__ void step(f32x4& acc, const uint4& qv, uint32_t sv, int st,
                                        int sc_dt, const uint4* xa, bool a_lane, const Masks& M) {
-    float sc = scale_value<SW>(sv, sc_dt);
-    if constexpr (MUnit<F>::INT) sc = round_act<ACT>(sc);
+    const float sc = applied_scale<F, ACT>(scale_value<SW>(sv, sc_dt));
     uint4 b[NMF];
     unit_b<F, ACT>(qv, sc, M, b);
     uint4 a[NMF];

@@ -495,11 +495,19 @@ def _prefill_unsupported(geom, act_dtype, scale_dtype, w_dtype):
     """Why the grouped prefill kernels cannot run this geometry, or None
     (vaayu/packed_expert_kernels.py:657-673): the decode rules, no fp32 activations, and
     an MFMA K step -- 4 lanes' 16-byte units -- that divides hidden and intermediate."""
-    if isinstance(geom[0], str):
-        return f"code format {geom[0]!r} (the prefill kernels take packed integer codes)"
     why = _unsupported(geom, act_dtype, scale_dtype, w_dtype)
     if why is not None:
         return why
+    if isinstance(geom[0], str):                 # FP8 e4m3 / MXFP4 blobs
+        if act_dtype == torch.float32:
+            return "fp32 activations (the matrix cores would run them at reduced precision)"
+        _fmt, bits, _group, _brows = geom_format(geom)
+        lay = _layout(geom)
+        step = 4 * (128 // bits)
+        for what, k in (("hidden", lay["gate"][3]), ("intermediate", lay["gate"][2])):
+            if k % step:
+                return f"{what} {k} is not a multiple of the {step}-code K tile"
+        return None
     bits, gs, _roles = geom
     lay = _layout(geom)
     inter, hid = lay["gate"][2], lay["gate"][3]
