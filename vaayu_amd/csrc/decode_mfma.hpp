@@ -92,11 +92,15 @@ struct ColumnDot {
   uint4 qa[NB], qb[NB];
   uint32_t sa[NB], sb[NB];
 
+  // Requests go out as (codes, scale) of step 0, then of step 1, ...: the wait counter is
+  // in order, so step i's dequant then waits only for steps 0..i, not for every code of the
+  // chunk (the scheduling barriers stop the compiler from grouping all code loads first).
   __device__ __forceinline__ void load(uint4 (&qv)[NB], uint32_t (&sv)[NB], int st0) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       qv[i] = buf_load16(P, cbase + (uint32_t)(st0 + i) * 64u);
       sv[i] = buf_load_scale<SW>(S, sbase + ((u0 + 4u * (uint32_t)(st0 + i)) >> ushift));
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
