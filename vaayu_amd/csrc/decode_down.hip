@@ -16,17 +16,21 @@ template <int F, int ACT, int SW>
 static int mfma_down_at(const void* h, const int64_t* tbl, const void* rw, int rw_dt, float* out,
                         const DownPlan& d, int w_round, hipStream_t st) {
   const int kps = d.kp == 4 ? 2 : d.kp == 2 ? 1 : 0;
-#define DN(NS_) hipLaunchKernelGGL((mfma_down_kernel<F, ACT, SW, NS_>), dim3(d.blocks), dim3(512), \
-                                   d.lds, st, tbl, h, rw, out, d.s, rw_dt, kps, d.ps, d.nrg,      \
-                                   w_round)
+  // one (row group, pair) per wave: the straight-line variant
+  const bool one = d.nrg == 1 && d.ps >= d.s.n_pairs;
+#define DN(NS_, ONE_) hipLaunchKernelGGL((mfma_down_kernel<F, ACT, SW, NS_, ONE_>), dim3(d.blocks), \
+                                         dim3(512), d.lds, st, tbl, h, rw, out, d.s, rw_dt, kps,  \
+                                         d.ps, d.nrg, w_round)
+#define DN2(NS_) if (one) DN(NS_, true); else DN(NS_, false)
   switch (d.s.steps) {
-    case 1: DN(1); break;
-    case 2: DN(2); break;
-    case 3: DN(3); break;
-    case 4: DN(4); break;
-    case 8: DN(8); break;
-    default: DN(0); break;
+    case 1: DN2(1); break;
+    case 2: DN2(2); break;
+    case 3: DN2(3); break;
+    case 4: DN2(4); break;
+    case 8: DN2(8); break;
+    default: DN(0, false); break;
   }
+#undef DN2
 #undef DN
   return 0;
 }

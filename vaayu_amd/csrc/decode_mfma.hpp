@@ -216,7 +216,7 @@ mfma_gate_up_kernel(const int64_t* __restrict__ tbl, const uint32_t* __restrict_
 // c_p = fl32(round(y) * w[slot]) (+ one rounding when the routing weight is in the
 // activation dtype) into LDS, and after one barrier the block sums each row's contributions
 // sequentially in table order. Nothing is atomic.
-template <int F, int ACT, int SW, int NS>
+template <int F, int ACT, int SW, int NS, bool ONE>
 __global__ void __launch_bounds__(512)
 mfma_down_kernel(const int64_t* __restrict__ tbl, const void* __restrict__ h,
                  const void* __restrict__ rw, float* __restrict__ out, MShape s, int rw_dt,
@@ -261,27 +261,47 @@ mfma_down_kernel(const int64_t* __restrict__ tbl, const void* __restrict__ h,
   }
   lds_barrier();
   const Masks M = make_masks();
-  for (int gi = 0; gi < nrg; ++gi) {
+  // One (row group, pair) of this wave: the dot, the K-part sum, the weighted contribution.
+  auto one = [&](int gi, int p, bool live) {
     const int brow = (gi * rg + g) * RW;                     // first row, in-block
-    for (int p = pl; p < s.n_pairs; p += ps) {
-      if (gi != 0 || p != pl) begin(gi, p);
-      const int64_t slot = tbl[3 * p + 2];
-      const uint4* xa = lds + p * p16 + (c * s.part_units + q) * (CPU / 8);
-      const f32x4 acc = cd.finish(s, xa, c < KP, M);
-      float v = kp == 0 ? acc[0] : kp == 1 ? acc[1] : kp == 2 ? acc[2] : acc[3];
-      if (KP == 4) v += dpp_move<kRowRor4>(v);
-      if (KP >= 2) v += dpp_move<kRowRor8>(v);
-      const float wgt = rw_dt == DT_FP32 ? load_as_float<DT_FP32>(rw, slot)
-                      : rw_dt == DT_BF16 ? load_as_float<DT_BF16>(rw, slot)
-                                         : load_as_float<DT_FP16>(rw, slot);
-      if (lane < RW) {
-        // The product is rounded to fp32 on its own (it goes to LDS before any add), as
-        // stock's `y * weight` then `out +=` are two roundings.
-        float cv = round_act<ACT>(v) * wgt;
-        if (w_round) cv = round_act<ACT>(cv);
-        cbuf[p * br + brow + lane] = cv;
-      }
+    const int64_t slot = tbl[3 * p + 2];
+    // The routing weight is requested before the dot's steps, so its latency overlaps them,
+    // as two 16-bit loads with no branch on its dtype (a branch there would wait for every
+    // request of the wave): the low half, and the high half of an fp32 weight (for a 16-bit
+    // weight the same half again). Both stay inside the weight's own bytes.
+    const int esz = rw_dt == DT_FP32 ? 4 : 2;
+    const uint16_t* wp = (const uint16_t*)((const char*)rw + slot * esz);
+    const uint16_t w_lo = wp[0];
+    const uint16_t w_hi = wp[esz == 4 ? 1 : 0];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4* xa = lds + p * p16 + (c * s.part_units + q) * (CPU / 8);
+    const f32x4 acc = cd.finish(s, xa, c < KP, M);
+    float v = kp == 0 ? acc[0] : kp == 1 ? acc[1] : kp == 2 ? acc[2] : acc[3];
+    if (KP == 4) v += dpp_move<kRowRor4>(v);
+    if (KP >= 2) v += dpp_move<kRowRor8>(v);
+    const float wgt = rw_dt == DT_FP32 ? __builtin_bit_cast(float, (uint32_t)w_hi << 16 | w_lo)
+                    : rw_dt == DT_BF16 ? __builtin_bit_cast(float, (uint32_t)w_lo << 16)
+                                       : (float)__builtin_bit_cast(_Float16, w_lo);
+    if (live && lane < RW) {
+      // The product is rounded to fp32 on its own (it goes to LDS before any add), as
+      // stock's `y * weight` then `out +=` are two roundings.
+      float cv = round_act<ACT>(v) * wgt;
+      if (w_round) cv = round_act<ACT>(cv);
+      cbuf[p * br + brow + lane] = cv;
     }
+  };
+  if constexpr (ONE) {
+    // One row group and at most one pair per wave (its requests went out before the
+    // staging barrier): straight code with no branch, so each step waits only for its own
+    // codes. An idle wave (pl >= n_pairs) computes pair 0 and writes nothing. Inside the
+    // loops below, the compiler waits for all of a wave's requests before its first step.
+    one(0, pl < s.n_pairs ? pl : 0, pl < s.n_pairs);
+  } else {
+    for (int gi = 0; gi < nrg; ++gi)
+      for (int p = pl; p < s.n_pairs; p += ps) {
+        if (gi != 0 || p != pl) begin(gi, p);
+        one(gi, p, true);
+      }
   }
   __syncthreads();
   for (int t = threadIdx.x; t < br; t += blockDim.x) {
