@@ -346,7 +346,7 @@ __device__ __forceinline__ void gate_up_run(const Item& it, const void* x,
                                             int top_k, int hidden, int inter, int gshift,
                                             int rshift, int sc_dt, int64_t gate_w,
                                             int64_t gate_s, int64_t up_w, int64_t up_s,
-                                            char* lds0, char* lds1) {
+                                            char* lds0, char* lds1, int* rid_s) {
   constexpr int BITS = CodeBits<F>::value;
   constexpr int KS = 512 / BITS;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -365,15 +365,20 @@ __device__ __forceinline__ void gate_up_run(const Item& it, const void* x,
     const int64_t rid = rrow[r];
     return rid >= 0 ? (uint32_t)(rid / top_k) * (uint32_t)hidden * 2u : kNoRow;
   });
+  // the run's row ids in LDS (the K loop's first barrier publishes them) for the epilogue
+  if (threadIdx.x < S * 16) rid_s[threadIdx.x] = (int)rrow[threadIdx.x];
   f32x4 acc[2][S];
   run_k<F, ACT, SW, 2, S>(role, rsrc(x, kNoRow), a, lds0, lds1, hidden, q, m, acc);
-  // C layout: lane (q, m) holds rows 4q..4q+3 of sub-tile s, column m.
+  // C layout: lane (q, m) holds rows 4q..4q+3 of sub-tile s, column m. The stores go out
+  // back to back (the row ids come from LDS, so no load waits between them).
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t r = rrow[s * 16 + 4 * q + i];
-      if (r >= 0 && n_ok) store_act<ACT>(h, r * inter + n, silu_mul<ACT>(acc[0][s][i], acc[1][s][i]));
+      const int r = rid_s[s * 16 + 4 * q + i];
+      if (r >= 0 && n_ok)
+        store_act<ACT>(h, (int64_t)r * inter + n, silu_mul<ACT>(acc[0][s][i], acc[1][s][i]));
+      if (i == 3) __builtin_amdgcn_sched_barrier(0);    // one sub-tile's ids live at a time
     }
 }
 
@@ -382,7 +387,7 @@ __device__ __forceinline__ void down_run(const Item& it, const void* h, const in
                                          const int64_t* tbl, const void* rw, int rw_dt, float* y,
                                          int hidden, int inter, int gshift, int rshift, int sc_dt,
                                          int64_t down_w, int64_t down_s, int w_round,
-                                         char* lds0, char* lds1) {
+                                         char* lds0, char* lds1, int* rid_s, float* w_s) {
   constexpr int BITS = CodeBits<F>::value;
   constexpr int KS = 512 / BITS;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -400,17 +405,37 @@ __device__ __forceinline__ void down_run(const Item& it, const void* h, const in
     const int64_t rid = rrow[r];
     return rid >= 0 ? (uint32_t)rid * (uint32_t)inter * 2u : kNoRow;
   });
+  // The run's row ids go to LDS now (the K loop's first barrier publishes them); the
+  // thread of each row also requests that row's routing weight now (two 16-bit loads, no
+  // branch on the dtype: the low half, and the high half of an fp32 weight) and puts it in
+  // LDS after the K loop. The epilogue then reads both from LDS: no load waits between its
+  // stores.
+  float w_mine = 0.f;
+  if (threadIdx.x < S * 16) {
+    const int rid = (int)rrow[threadIdx.x];
+    rid_s[threadIdx.x] = rid;
+    const int esz = rw_dt == DT_FP32 ? 4 : 2;
+    const uint16_t* wp = (const uint16_t*)((const char*)rw + (int64_t)max(rid, 0) * esz);
+    const uint16_t w_lo = wp[0];
+    const uint16_t w_hi = wp[esz == 4 ? 1 : 0];
+    w_mine = rw_dt == DT_FP32 ? __builtin_bit_cast(float, (uint32_t)w_hi << 16 | w_lo)
+           : rw_dt == DT_BF16 ? __builtin_bit_cast(float, (uint32_t)w_lo << 16)
+                              : (float)__builtin_bit_cast(_Float16, w_lo);
+  }
   f32x4 acc[1][S];
   run_k<F, ACT, SW, 1, S>(role, rsrc(h, kNoRow), a, lds0, lds1, inter, q, m, acc);
+  if (threadIdx.x < S * 16) w_s[threadIdx.x] = w_mine;
+  __syncthreads();
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t r = rrow[s * 16 + 4 * q + i];
+      const int t = s * 16 + 4 * q + i;
+      const int r = rid_s[t];
       if (r >= 0 && n_ok) {
-        float c = round_act<ACT>(acc[0][s][i]) * load_dt(rw, r, rw_dt);
+        float c = round_act<ACT>(acc[0][s][i]) * w_s[t];
         if (w_round) c = round_act<ACT>(c);
-        y[r * hidden + n] = c;
+        y[(int64_t)r * hidden + n] = c;
       }
     }
 }
@@ -437,8 +462,10 @@ prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ r
   __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / BITS)];
   __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / BITS)];
   const Item it = item_here<kRunGateUp>(tbl, n_blocks, n_tiles);
+  __shared__ int rid_s[kRunGateUp * 16];
 #define GU_CALL(S_) gate_up_run<F, ACT, SW, S_>(it, x, rows, tbl, h, top_k, hidden, inter, gshift, \
-                                            rshift, sc_dt, gate_w, gate_s, up_w, up_s, lds0, lds1)
+                                            rshift, sc_dt, gate_w, gate_s, up_w, up_s, lds0, lds1, \
+                                            rid_s)
   VAAYU_BY_S8(GU_CALL)
 #undef GU_CALL
 }
@@ -454,8 +481,11 @@ prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows
   __shared__ __align__(1024) char lds0[kRunDown * 16 * (2 * 512 / BITS)];
   __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / BITS)];
   const Item it = item_here<kRunDown>(tbl, n_blocks, n_tiles);
+  __shared__ int rid_s[kRunDown * 16];
+  __shared__ float w_s[kRunDown * 16];
 #define DN_CALL(S_) down_run<F, ACT, SW, S_>(it, h, rows, tbl, rw, rw_dt, y, hidden, inter, gshift, \
-                                         rshift, sc_dt, down_w, down_s, w_round, lds0, lds1)
+                                         rshift, sc_dt, down_w, down_s, w_round, lds0, lds1, \
+                                         rid_s, w_s)
   VAAYU_BY_S8(DN_CALL)
 #undef DN_CALL
 }
