@@ -149,6 +149,9 @@ WORKLOADS = {
                                   "experts with fp32 scales per 128 x 128 block", fmt="e4m3"),
     "qwen3-mxfp4-decode": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, MXFP4 "
                                     "e2m1 experts with E8M0 scales per 32", fmt="mxfp4"),
+    "qwen3-decode-routed": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, int4 g128 "
+                                     "fp16 scales, router matmul + softmax top-k + pair table on "
+                                     "the GPU in the same graph", fmt="int4", routed=True),
     "dsv3-prefill": dict(name="DeepSeek-V3-shape MoE layer prefill, 2048 tokens", hidden=7168,
                          inter=2048, experts=256, top_k=8, tokens=2048, routing="zipf",
                          shared=True, bound="mfma"),
@@ -458,6 +461,28 @@ def main():
     gu_only = capture(gate_up)
     dn_only = capture(down)
 
+    # ── routed: the router product, the routing and the pair table on the GPU too ───────
+    routed_layer = None
+    if spec is not None and spec.get("routed"):
+        from vaayu_amd.device_routing import ResidentExperts
+        rg = torch.Generator(device=dev).manual_seed(7)
+        rxs = [ResidentExperts(layers[l]) for l in range(L)]
+        # the router's weight stored transposed ([hidden, experts], contiguous)
+        w_rt = [(torch.randn(H, E, generator=rg, device=dev) * 0.05).to(torch.bfloat16)
+                for _ in range(L)]
+        r_logits = [torch.empty(1, E, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+        r_bufs = [rx.buffers(K, x.dtype) for rx in rxs]
+        r_outs = [torch.empty(1, H, dtype=torch.float32, device=dev) for _ in range(L)]
+
+        def routed_layer(l, _stream):
+            torch.matmul(x, w_rt[l], out=r_logits[l])
+            rxs[l].decode(x, r_logits[l], K, r_outs[l], bufs=r_bufs[l])
+
+        for l in range(L):
+            routed_layer(l, st)
+        torch.cuda.synchronize()
+        routed_graph = capture(routed_layer)
+
     def time_graph(graph, steps, warmup):
         for _ in range(warmup):
             graph.replay()
@@ -476,6 +501,14 @@ def main():
     us_tok_layer = ms_step * 1000.0 / L
     log(f"step {ms_step:.3f} ms = {us_tok_layer:.2f} us/token/layer; gate_up "
         f"{ms_gu * 1000 / L:.2f} us, down {ms_dn * 1000 / L:.2f} us per launch")
+    routed_extra = None
+    if routed_layer is not None:
+        ms_routed = time_graph(routed_graph, args.steps, args.warmup)
+        routed_extra = {"expert_kernels_us_per_layer": round(us_tok_layer, 3),
+                        "router_and_routing_us_per_layer":
+                            round((ms_routed - ms_step) * 1000.0 / L, 3)}
+        ms_step, us_tok_layer = ms_routed, ms_routed * 1000.0 / L
+        log(f"routed step {ms_step:.3f} ms = {us_tok_layer:.2f} us/token/layer {routed_extra}")
 
     # algorithmic bytes (distinct routed experts' codes + scales + activations)
     from vaayu_amd.block_formats import geom_format
@@ -500,6 +533,18 @@ def main():
     got = outs[0].cpu().numpy()
     parity = {"relL2": O.rel_l2(got, ref), "max_abs": float(np.abs(got - ref).max()),
               "tolerance": {"relL2": 5e-3, "max_abs": 2e-2}}
+    if routed_layer is not None:             # layer 0 as routed on the GPU
+        want_w, want_ids = O.route_softmax_topk(r_logits[0].cpu().float(), K)
+        got_ids, got_w = r_bufs[0].ids.cpu().numpy(), r_bufs[0].weights.cpu()
+        e = got_ids[0].tolist()
+        pairs = [({"flat": {n: t.cpu() for n, t in layers[0][e[s]]["flat"].items()},
+                   "geom": geom}, s) for s in sorted(range(K), key=e.__getitem__)]
+        ref = O.stock_decode(x.cpu(), pairs, got_w)
+        got = r_outs[0].cpu().numpy()
+        parity["routed"] = {
+            "ids_equal": bool(np.array_equal(got_ids, want_ids)),
+            "weights_max_rel": float(np.abs(got_w.numpy() - want_w).max() / np.abs(want_w).max()),
+            "relL2": O.rel_l2(got, ref), "max_abs": float(np.abs(got - ref).max())}
     log(f"parity layer 0 vs oracle: {parity}")
 
     # ── CPU baseline: the stock loop on torch CPU, bounded sample ───────────────────────
@@ -551,6 +596,8 @@ def main():
         "parity": parity,
         "cpu_baseline": cpu,
     }
+    if routed_extra is not None:
+        result["routed"] = routed_extra
     print(json.dumps(result), flush=True)
 
 

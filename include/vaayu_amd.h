@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 2
+#define VAAYU_ABI_VERSION 3
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -131,6 +131,34 @@ int vaayu_dequant_fp8_block(const uint8_t *weight, const void *scale, int32_t sc
  * [rows, k] of out_dtype 0 bf16, 1 fp16, 2 fp32. Bit-exact. */
 int vaayu_upcast_mx(const uint8_t *q, int32_t fmt, const uint8_t *scale, void *out,
                     int32_t out_dtype, int64_t rows, int64_t k, void *stream);
+
+/* Router top-k on the GPU, the decode-time expert budget, and the one-token decode table
+ * built from them. Replaces the reference's default routing,
+ * `torch.topk(logits.float().softmax(-1), k)` then `w / w.sum(-1)` (the `_route` branch for a
+ * router returning bare logits, vaayu/moe_patch.py:2329-2334, and `route_experts`' fallback,
+ * :159-161), `truncate_top_k(w, idx, keep_k, top_p)` on it (vaayu/moe_patch.py:170-215),
+ * and the host round trip that sorts the slots by expert id and builds `_table_values`
+ * (vaayu/moe_patch.py:2386-2389, vaayu/packed_expert_kernels.py:349-352) -- for experts
+ * that are all resident.
+ * logits       [tokens, experts] of logits_dtype (0 bf16, 1 fp16, 2 fp32), contiguous
+ * top_k        the router's k; keep_k: the slots kept (n_out = min(keep_k, top_k), the k
+ *              largest, rescaled to the row's original sum); top_p: 0 = off, else keep the
+ *              fewest slots whose normalised weight reaches top_p and re-point each dropped
+ *              slot at the top-1 expert with weight 0
+ * weights      fp32 [tokens, n_out] <- the softmax probabilities of the picks in descending
+ *              order (ties to the lower expert id), divided by their sum when renorm != 0,
+ *              then the budget above
+ * ids          int64 [tokens, n_out] <- their expert ids
+ * expert_table int64 [experts, 2]: (packed address, scale address) of each expert's blob
+ * pair_table   int64 [n_out * 3] or NULL; with tokens == 1 <- (packed address, scale
+ *              address, slot) per slot in the stable (expert id, slot) order: the decode
+ *              entries' table
+ * experts 1..1024, top_k 1..min(16, experts), keep_k >= 1, top_p >= 0. NaN logits give NaN
+ * weights. */
+int vaayu_route_topk(const void *logits, int32_t logits_dtype, int32_t tokens, int32_t experts,
+                     int32_t top_k, int32_t keep_k, float top_p, int32_t renorm, float *weights,
+                     int64_t *ids, const int64_t *expert_table, int64_t *pair_table,
+                     void *stream);
 
 #ifdef __cplusplus
 }

@@ -470,6 +470,47 @@ def route_softmax_topk(logits, top_k: int):
     return (w / w.sum(axis=-1, keepdims=True)).astype(np.float32), idx.astype(np.int64)
 
 
+def truncate_top_k(weights, indices, k=None, p=None):
+    """The decode-time expert budget `truncate_top_k` (vaayu/moe_patch.py:170-215) on
+    routed (weights, indices) [..., K]: keep the k largest weights (rescaled to the row's
+    original sum), then with p keep per row the fewest slots whose normalised weight
+    reaches p (the mass BEFORE a slot < p keeps it), re-pointing each dropped slot at the
+    row's top-1 expert with weight 0. The original sum snaps to 1.0 within 1e-2. Equal
+    weights order by slot (stable); sums run in slot order, in fp32."""
+    w = np.array(to_np(weights), dtype=np.float32)
+    idx = np.array(to_np(indices), dtype=np.int64)
+    n = w.shape[-1]
+    if (k is None or k >= n) and p is None:
+        return w, idx
+
+    def ssum(a):                                   # slot-order fp32 sum over the last axis
+        acc = np.zeros(a.shape[:-1] + (1,), dtype=np.float32)
+        for j in range(a.shape[-1]):
+            acc = (acc + a[..., j:j + 1]).astype(np.float32)
+        return acc
+
+    total = ssum(w)
+    total = np.where(np.abs(total - np.float32(1)) < np.float32(1e-2), np.float32(1), total)
+    if k is not None and k < n:
+        pos = np.argsort(-w, axis=-1, kind="stable")[..., :k]
+        wk = np.take_along_axis(w, pos, -1)
+        w = (wk / ssum(wk) * total).astype(np.float32)
+        idx = np.take_along_axis(idx, pos, -1)
+    if p is None:
+        return w, idx
+    wn = (w / ssum(w)).astype(np.float32)
+    order = np.argsort(-wn, axis=-1, kind="stable")
+    ws = np.take_along_axis(wn, order, -1)
+    cs = np.cumsum(ws, axis=-1, dtype=np.float32)
+    keep_sorted = (cs - ws).astype(np.float32) < np.float32(p)
+    keep = np.zeros_like(keep_sorted)
+    np.put_along_axis(keep, order, keep_sorted, -1)
+    top1 = np.broadcast_to(np.take_along_axis(idx, order[..., :1], -1), idx.shape)
+    wk = np.where(keep, wn, np.float32(0)).astype(np.float32)
+    w = (wk / ssum(wk) * total).astype(np.float32)
+    return w, np.where(keep, idx, top1)
+
+
 # ── FP8 block-scaled and MXFP4 formats ──────────────────────────────────────────────────
 
 def e4m3_value(byte) -> np.ndarray:

@@ -341,6 +341,92 @@ def test_softmax_topk_renorm_brute_force_and_ties():
         assert np.allclose(w[r], [t / sum(top) for t in top], rtol=1e-6)
 
 
+# truncate_top_k: the reference's known answers (tests/test_decode_top_k.py:393-433) and
+# what the definition fixes by brute force over every kept subset.
+
+def test_truncate_cutoff_repoints_dropped_slots_at_the_top1():
+    w, i = O.truncate_top_k([[0.5, 0.3, 0.15, 0.05]], [[7, 3, 9, 1]], None, p=0.9)
+    assert i.tolist() == [[7, 3, 9, 7]] and w[0, 3] == 0.0
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
+def test_truncate_cutoff_finds_the_top1_by_weight_on_unsorted_routing():
+    w, i = O.truncate_top_k([[0.05, 0.5, 0.15, 0.3]], [[1, 7, 9, 3]], None, p=0.9)
+    assert i.tolist() == [[7, 7, 9, 3]] and w[0, 0] == 0.0
+
+
+def test_truncate_cutoff_always_keeps_the_top1():
+    w, i = O.truncate_top_k([[0.4, 0.3, 0.2, 0.1]], [[5, 6, 7, 8]], None, p=0.01)
+    assert set(i.flatten().tolist()) == {5} and abs(float(w[0, 0]) - 1.0) < 1e-6
+
+
+def test_truncate_off_path_is_unchanged():
+    w = np.random.default_rng(0).random((3, 8)).astype(np.float32)
+    w /= w.sum(-1, keepdims=True)
+    i = np.arange(24).reshape(3, 8)
+    a, b = O.truncate_top_k(w, i, 8, None)
+    assert np.array_equal(a, w) and np.array_equal(b, i)
+
+
+@pytest.mark.parametrize("experts,top_k", [(128, 8), (256, 8), (512, 10)])
+def test_truncate_keeps_the_k_largest_renormalised(experts, top_k):
+    """tests/test_decode_top_k.py:36-70: the kept experts are the k largest weights, and
+    the kept weights sum to the original (unit) sum."""
+    rng = np.random.default_rng(experts)
+    w, idx = O.route_softmax_topk(rng.standard_normal((7, experts)).astype(np.float32), top_k)
+    k = top_k - 2
+    wt, it = O.truncate_top_k(w, idx, k)
+    assert wt.shape == it.shape == (7, k)
+    for r in range(7):
+        assert set(it[r].tolist()) == set(idx[r][np.argsort(-w[r], kind="stable")[:k]].tolist())
+    assert np.allclose(wt.sum(-1), 1.0, atol=1e-5)
+
+
+def test_truncate_p_is_the_fewest_slots_reaching_p_brute_force():
+    """p keeps the smallest prefix of the weight-sorted slots whose mass reaches p: checked
+    against every prefix length, on rows whose cumulative sums are far from p."""
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        w = rng.random(6).astype(np.float32)
+        w /= w.sum()
+        idx = rng.permutation(64)[:6]
+        p = float(rng.uniform(0.05, 0.95))
+        srt = np.sort(w)[::-1]
+        if np.min(np.abs(np.cumsum(srt) - p)) < 1e-4:
+            continue
+        n_keep = next(n for n in range(1, 7) if srt[:n].sum() >= p)
+        wt, it = O.truncate_top_k(w[None], idx[None], None, p)
+        kept = wt[0] > 0
+        assert kept.sum() == n_keep
+        assert set(it[0][kept].tolist()) == set(idx[np.argsort(-w)[:n_keep]].tolist())
+        assert (it[0][~kept] == idx[np.argmax(w)]).all()
+        assert np.isclose(wt[0].sum(), 1.0, atol=1e-6)
+        assert np.allclose(wt[0][kept], w[kept] / w[kept].sum(), rtol=1e-5)
+
+
+def test_truncate_rescales_to_the_original_sum():
+    """A row that does not sum to 1 (a scaled router) keeps its sum; one within 1e-2 of 1
+    snaps to exactly 1."""
+    w = np.array([[0.8, 0.6, 0.4, 0.2]], np.float32)            # sums to 2
+    wt, _ = O.truncate_top_k(w, [[0, 1, 2, 3]], 2)
+    assert np.allclose(wt, [[0.8 / 1.4 * 2, 0.6 / 1.4 * 2]], rtol=1e-6)
+    w = np.array([[0.5, 0.3, 0.1, 0.095]], np.float32)           # sums to 0.995
+    wt, _ = O.truncate_top_k(w, [[0, 1, 2, 3]], 2)
+    assert np.allclose(wt.sum(), 1.0, atol=1e-7)
+
+
+def test_host_truncate_matches_the_oracle():
+    """The package's host `truncate_top_k` (torch) against the oracle on routed rows."""
+    from vaayu_amd.moe_patch import truncate_top_k as host
+    rng = np.random.default_rng(5)
+    w, idx = O.route_softmax_topk(rng.standard_normal((32, 128)).astype(np.float32), 8)
+    for k, p in [(6, None), (None, 0.7), (5, 0.6), (8, 0.5)]:
+        hw, hi = host(torch.from_numpy(w), torch.from_numpy(idx), k, p)
+        ow, oi = O.truncate_top_k(w, idx, k, p)
+        assert np.array_equal(hi.numpy(), oi)
+        np.testing.assert_allclose(hw.numpy(), ow, rtol=1e-6, atol=1e-7)
+
+
 # ── FP8 block-scaled and MXFP4 ──────────────────────────────────────────────────────────
 
 def test_e4m3_exhaustive():
