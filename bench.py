@@ -158,6 +158,10 @@ WORKLOADS = {
     "mixtral-prefill": dict(name="Mixtral-8x7B-shape MoE layer prefill, 512 tokens", hidden=4096,
                             inter=14336, experts=8, top_k=2, tokens=512, routing="softmax",
                             shared=False, bound="mfma"),
+    "qwen3next-gdn-decode": dict(name="Qwen3-Next-80B-shape gated-delta mixer decode, 1 token: "
+                                      "conv update + recurrent rule + gated norm",
+                                 gdn=True, HV=32, HK=16, K=128, V=128, W=4, mixers=36,
+                                 copies=8),
     "qwen3-decode-b8": dict(name="Qwen3-30B-A3B-shape MoE layer decode, batch of 8 tokens",
                             hidden=2048, inter=768, experts=128, top_k=8, tokens=8,
                             routing="softmax", shared=False, bound="hbm"),
@@ -359,6 +363,138 @@ def bench_prefill(args, spec):
     print(json.dumps(result), flush=True)
 
 
+def bench_gdn(args, spec):
+    """A gated-delta mixer's decode step (conv update -> recurrent rule -> gated norm) for
+    `mixers` x `copies` mixers with their own HBM-resident states, recorded in one graph."""
+    import vaayu_amd.gated_delta_kernels as gdk
+    from oracle import gated_delta as G
+    from oracle import oracle as O
+
+    if gdk.triton is None:
+        raise SystemExit("vaayu_amd kernel library missing: run `python -m vaayu_amd.build`")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    HV, HK, K, V, W = spec["HV"], spec["HK"], spec["K"], spec["V"], spec["W"]
+    D = 2 * HK * K + HV * V
+    n = spec["mixers"] * spec["copies"]
+    gen = torch.Generator(device=dev).manual_seed(5)
+
+    def rnd(*shape, dtype=torch.bfloat16, s=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * s).to(dtype)
+
+    mix = [dict(conv_state=rnd(1, W, D).transpose(1, 2), conv_w=rnd(D, W, s=0.3),
+                h=rnd(1, HV, K, V, dtype=torch.float32, s=0.1),
+                norm_w=(1 + rnd(V, dtype=torch.float32, s=0.1)).bfloat16(),
+                x=rnd(1, 1, D).transpose(1, 2), g=-torch.rand(1, 1, HV, device=dev),
+                beta=torch.rand(1, 1, HV, device=dev).bfloat16(), z=rnd(1, 1, HV, V))
+           for _ in range(n)]
+    log(f"{n} mixers, states {n * (HV * K * V * 4 + D * W * 2) / 1e9:.2f} GB")
+
+    def step(m):
+        qkv = gdk.fused_conv_update(m["x"], m["conv_state"], m["conv_w"])[..., 0]
+        q, k, v = torch.split(qkv, [HK * K, HK * K, HV * V], -1)
+        q = q.reshape(1, 1, HK, K).repeat_interleave(HV // HK, 2)
+        k = k.reshape(1, 1, HK, K).repeat_interleave(HV // HK, 2)
+        o, m["ht"] = gdk.fused_recurrent_rule(q, k, v.reshape(1, 1, HV, V), m["g"], m["beta"],
+                                              m["h"], True, True)
+        m["out"] = gdk.fused_gated_norm(m["norm_w"], 1e-6, o, m["z"])
+
+    def rule_only(m):
+        gdk.fused_recurrent_rule(m["q"], m["k"], m["v"], m["g"], m["beta"], m["h"], True, True)
+
+    for m in mix:                               # eager once; inputs for the rule-only graph
+        saved = m["conv_state"].clone()
+        step(m)
+        m["conv_state"].copy_(saved)
+        m["q"] = rnd(1, 1, HV, K)
+        m["k"] = rnd(1, 1, HV, K)
+        m["v"] = rnd(1, 1, HV, V)
+    torch.cuda.synchronize()
+
+    def capture(body):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for m in mix:
+                body(m)
+        return graph
+
+    def time_graph(graph):
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
+
+    ms_step = time_graph(capture(step))
+    ms_rule = time_graph(capture(rule_only))
+    us_mixer, us_rule = ms_step * 1000 / n, ms_rule * 1000 / n
+    rule_bytes = 2 * HV * K * V * 4 + 2 * HV * K * 2 + 2 * HV * V * 2 + HV * 8
+    gbs = rule_bytes / (us_rule * 1e-6) / 1e9
+    log(f"mixer step {us_mixer:.2f} us; rule kernel {us_rule:.2f} us per launch = {gbs:.0f} GB/s")
+
+    # parity of one mixer's step against the oracle (conv -> rule -> norm, inputs from the
+    # step itself so each stage is checked on what it was given)
+    m = mix[0]
+    st0 = m["conv_state"].clone()
+    qkv = gdk.fused_conv_update(m["x"], m["conv_state"], m["conv_w"])
+    ro, _rs = G.gdn_conv_update(m["x"], st0, m["conv_w"])
+    q, k, v = torch.split(qkv[..., 0], [HK * K, HK * K, HV * V], -1)
+    q = q.reshape(1, 1, HK, K).repeat_interleave(HV // HK, 2)
+    k = k.reshape(1, 1, HK, K).repeat_interleave(HV // HK, 2)
+    o, ht = gdk.fused_recurrent_rule(q, k, v.reshape(1, 1, HV, V), m["g"], m["beta"], m["h"],
+                                     True, True)
+    r_o, r_h = G.gdn_rule(q, k, v.reshape(1, 1, HV, V), m["g"], m["beta"], m["h"])
+    out = gdk.fused_gated_norm(m["norm_w"], 1e-6, o, m["z"])
+    r_n = G.gdn_gated_norm(o, m["z"], m["norm_w"], 1e-6, "bf16", True)
+    parity = {"conv_relL2": O.rel_l2(O.to_np(qkv), ro), "rule_relL2": O.rel_l2(O.to_np(o), r_o),
+              "state_relL2": O.rel_l2(O.to_np(ht), r_h),
+              "norm_relL2": O.rel_l2(O.to_np(out), r_n)}
+    log(f"parity vs oracle: {parity}")
+
+    cpu = None
+    if not args.no_cpu:
+        xs = [{k_: O.to_np(t) for k_, t in mix[i].items() if isinstance(t, torch.Tensor)}
+              for i in range(4)]
+        n_calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            c = xs[n_calls % 4]
+            qkv_c, _ = G.gdn_conv_update(c["x"], c["conv_state"], c["conv_w"])
+            qc, kc, vc = np.split(qkv_c[..., 0], [HK * K, 2 * HK * K], -1)
+            qc = np.repeat(qc.reshape(1, 1, HK, K), HV // HK, 2)
+            kc = np.repeat(kc.reshape(1, 1, HK, K), HV // HK, 2)
+            oc, _ = G.gdn_rule(qc, kc, vc.reshape(1, 1, HV, V), c["g"], c["beta"], c["h"])
+            G.gdn_gated_norm(oc, c["z"], c["norm_w"], 1e-6)
+            n_calls += 1
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(cpu_s * 1e6 / n_calls, 1), "unit": "us per mixer decode step",
+               "cores": 1, "kind": "port",
+               "sample": f"{n_calls} mixer steps through the oracle (numpy, float64), "
+                         f"{cpu_s:.1f} s"}
+        log(f"cpu baseline {cpu}")
+
+    result = {
+        "metric": "gated-delta mixer decode µs/token (conv + rule + norm)",
+        "value": round(us_mixer, 3), "unit": "us/token per mixer", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": spec["name"] + f", {n} HBM-resident mixer states per step",
+                   "num_v_heads": HV, "num_k_heads": HK, "head_k_dim": K, "head_v_dim": V,
+                   "conv_width": W, "conv_dim": D, "mixers": n, "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "gdn_rule_kernel", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": rule_bytes,
+                     "us_per_launch": round(us_rule, 3)},
+        "parity": parity, "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize:
@@ -371,6 +507,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     spec = WORKLOADS[args.workload]
+    if spec is not None and spec.get("gdn"):
+        bench_gdn(args, spec)
+        return
     if spec is not None and "tokens" in spec:
         bench_prefill(args, spec)
         return

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 3
+#define VAAYU_ABI_VERSION 4
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -159,6 +159,46 @@ int vaayu_route_topk(const void *logits, int32_t logits_dtype, int32_t tokens, i
                      int32_t top_k, int32_t keep_k, float top_p, int32_t renorm, float *weights,
                      int64_t *ids, const int64_t *expert_table, int64_t *pair_table,
                      void *stream);
+
+/* Gated-delta-net decode kernels (ABI 4). dtype codes 0 bf16, 1 fp16, 2 fp32. */
+
+/* The recurrent gated delta rule over T steps: replaces the reference's `_rule_kernel` /
+ * `fused_recurrent_rule` (vaayu/gated_delta_kernels.py:66-133), the drop-in for
+ * transformers' `torch_recurrent_gated_delta_rule`. Per (batch, value head):
+ *   h *= exp(g); delta = (v - h^T k) * beta; h += k delta^T; o = h^T q
+ * with q, k l2-normalised in fp32 (eps 1e-6) when l2norm != 0 and q scaled by `scale`.
+ * q, k [B, T, HV, K] and v [B, T, HV, V] of act_dtype, last dim contiguous; g, beta
+ * [B, T, HV] (g_dtype, beta_dtype); h0 [B, HV, K, V] of h0_dtype or NULL (zeros);
+ * o [B, T, HV, V] act_dtype, contiguous; ht fp32 [B, HV, K, V] contiguous or NULL.
+ * strides: 19 element strides -- q (b, t, h), k (b, t, h), v (b, t, h), g (b, t, h),
+ * beta (b, t, h), h0 (b, h, k, v). K <= 256, B * HV <= 65535. */
+int vaayu_gdn_rule(const void *q, const void *k, const void *v, const void *g,
+                   const void *beta, const void *h0, void *o, float *ht,
+                   const int64_t *strides, int32_t B, int32_t T, int32_t HV, int32_t K,
+                   int32_t V, float scale, int32_t act_dtype, int32_t g_dtype,
+                   int32_t beta_dtype, int32_t h0_dtype, int32_t l2norm, void *stream);
+
+/* The one-token causal depthwise conv update: replaces `_conv_kernel` /
+ * `fused_conv_update` (vaayu/gated_delta_kernels.py:136-190), the drop-in for transformers'
+ * `causal_conv1d_update` at one token. Shifts `state` [B, D, W] left one slot in place and
+ * appends x, every value passing through the weight dtype; o [B, D] (x_dtype, contiguous)
+ * <- silu(round_w(sum_j state_j w_j + bias)), rounded to the weight dtype.
+ * x [B, D, 1]; w [D, W]; bias [D] or NULL. strides: x (b, d), state (b, d, w), w (d, w).
+ * B <= 65535. */
+int vaayu_gdn_conv_update(const void *x, void *state, const void *w, const void *bias, void *o,
+                          const int64_t *strides, int32_t B, int32_t D, int32_t W,
+                          int32_t x_dtype, int32_t state_dtype, int32_t w_dtype,
+                          int32_t bias_dtype, void *stream);
+
+/* The gated RMSNorm of a gated-delta mixer: replaces `_norm_kernel` / `fused_gated_norm`
+ * (vaayu/gated_delta_kernels.py:197-235), the drop-in for `*RMSNormGated.forward(x, gate)`.
+ * Per row of N: y = round_x(x * rsqrt(mean(x^2) + eps)); y = w * y (rounded to x's dtype
+ * when round_mid != 0); o = round_x(y * silu(z)). x, z [rows, N] with strides (row, n); w [N]
+ * with stride; o [rows, N] x_dtype, contiguous. strides: x (r, n), z (r, n), w. */
+int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
+                         const int64_t *strides, int64_t rows, int32_t N, float eps,
+                         int32_t x_dtype, int32_t z_dtype, int32_t w_dtype, int32_t round_mid,
+                         void *stream);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -18,7 +18,7 @@ DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 EXPORTS = ("vaayu_abi_version", "vaayu_last_error", "vaayu_decode_gate_up", "vaayu_decode_down",
            "vaayu_prefill_gate_up", "vaayu_prefill_down", "vaayu_prefill_reduce",
            "vaayu_dequant_blob", "vaayu_dequant_fp8_block", "vaayu_upcast_mx",
-           "vaayu_route_topk")
+           "vaayu_route_topk", "vaayu_gdn_rule", "vaayu_gdn_conv_update", "vaayu_gdn_gated_norm")
 
 
 class Geom(ctypes.Structure):
@@ -56,6 +56,12 @@ def _bind(lib):
         "vaayu_upcast_mx": (ctypes.c_int, [vp, i32, vp, vp, i32, i64, i64, vp]),
         "vaayu_route_topk": (ctypes.c_int, [vp, i32, i32, i32, i32, i32, ctypes.c_float, i32,
                                              vp, vp, vp, vp, vp]),
+        "vaayu_gdn_rule": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
+                                          i32, ctypes.c_float, i32, i32, i32, i32, i32, vp]),
+        "vaayu_gdn_conv_update": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32,
+                                                 i32, i32, i32, vp]),
+        "vaayu_gdn_gated_norm": (ctypes.c_int, [vp, vp, vp, vp, vp, i64, i32, ctypes.c_float,
+                                                i32, i32, i32, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
