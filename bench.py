@@ -162,6 +162,10 @@ WORKLOADS = {
                                       "conv update + recurrent rule + gated norm",
                                  gdn=True, HV=32, HK=16, K=128, V=128, W=4, mixers=36,
                                  copies=8),
+    "gptoss-20b-prefill": dict(name="gpt-oss-20b-shape fused-3D MXFP4 MoE layer prefill, 2048 "
+                                    "tokens (32 experts, hidden 2880, inter 2880, top-4)",
+                               fused3d=True, hidden=2880, inter=2880, experts=32, top_k=4,
+                               tokens=2048),
     "qwen3-decode-b8": dict(name="Qwen3-30B-A3B-shape MoE layer decode, batch of 8 tokens",
                             hidden=2048, inter=768, experts=128, top_k=8, tokens=8,
                             routing="softmax", shared=False, bound="hbm"),
@@ -363,6 +367,121 @@ def bench_prefill(args, spec):
     print(json.dumps(result), flush=True)
 
 
+def bench_fused3d(args, spec):
+    """gpt-oss fused-3D MXFP4 experts: the two grouped GEMMs + the slot reduce over one
+    call's prepared tables, recorded in one graph."""
+    import vaayu_amd.packed_expert_kernels as pk
+    from vaayu_amd.fused3d import Fused3DExperts
+    from oracle import fused3d as F3
+    from oracle import oracle as O
+
+    if pk.triton is None:
+        raise SystemExit("vaayu_amd kernel library missing: run `python -m vaayu_amd.build`")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, I, E, K, T = spec["hidden"], spec["inter"], spec["experts"], spec["top_k"], spec["tokens"]
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def codes(*shape):
+        return torch.randint(0, 256, shape, generator=gen, device=dev, dtype=torch.uint8)
+
+    def scales(*shape):                    # 2^-10 .. 2^-6 per 32 codes: O(1) activations
+        return torch.randint(117, 122, shape, generator=gen, device=dev).to(torch.uint8)
+
+    layer = dict(gu_blocks=codes(E, 2 * I, H // 32, 16), gu_scales=scales(E, 2 * I, H // 32),
+                 gu_bias=torch.randn(E, 2 * I, generator=gen, device=dev) * 0.1,
+                 dn_blocks=codes(E, H, I // 32, 16), dn_scales=scales(E, H, I // 32),
+                 dn_bias=torch.randn(E, H, generator=gen, device=dev) * 0.1)
+    mod = Fused3DExperts(layer["gu_blocks"], layer["gu_scales"], layer["gu_bias"],
+                         layer["dn_blocks"], layer["dn_scales"], layer["dn_bias"])
+    wbytes = sum(t.numel() * t.element_size() for t in layer.values())
+    log(f"{E} experts resident: {wbytes / 1e9:.2f} GB")
+    cg = torch.Generator().manual_seed(99)
+    x = torch.randn(T, H, generator=cg).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=cg)
+    top, eidx = torch.topk(logits, K, dim=-1)        # gpt-oss: top-k logits, softmax of them
+    w = torch.softmax(top, dim=-1).to(dev)
+    tables = tuple(t.clone() if isinstance(t, torch.Tensor) else t for t in mod.tables(eidx))
+    xp = torch.zeros(T, mod.Hp, dtype=torch.bfloat16, device=dev)
+    xp[:, :H] = x
+    h = torch.zeros(T * K, mod.Ip, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(T * K, H, dtype=torch.float32, device=dev)
+    out = torch.empty(T, H, dtype=torch.float32, device=dev)
+    gammas = w.reshape(-1).float().contiguous()
+
+    def run():
+        mod.launch(xp, h, y, out, tables, gammas, K)
+
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    steps = max(1, args.steps // 5)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    flops = 2 * T * K * 3 * H * I
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"layer {ms * 1000:.1f} us = {ms * 1000 / T:.3f} us/token; {tflops:.1f} TFLOP/s "
+        f"({tflops / MFMA_PEAK_TFLOPS:.1%} of bf16 MFMA peak)")
+
+    # parity: two tokens against the oracle
+    got = out.to(torch.bfloat16).float().cpu().numpy()
+    lay_cpu = {k_: v.cpu() for k_, v in layer.items()}
+    worst = {"relL2": 0.0, "max_abs": 0.0}
+    for t in (0, T - 1):
+        ref = F3.fused3d_experts(x[t:t + 1].cpu(), eidx[t:t + 1], w[t:t + 1].cpu(), **lay_cpu)
+        worst["relL2"] = max(worst["relL2"], O.rel_l2(got[t:t + 1], ref))
+        worst["max_abs"] = max(worst["max_abs"], float(np.abs(got[t:t + 1] - ref).max()))
+    parity = dict(worst, tokens_checked=2, tolerance={"relL2": 5e-3, "max_abs": 2e-2})
+    log(f"parity vs oracle: {parity}")
+
+    cpu = None
+    if not args.no_cpu:
+        wgu, wdn = {}, {}                       # the first 8 tokens' experts, dequantized
+        for e in sorted(set(eidx[:8].reshape(-1).tolist())):
+            wgu[e] = F3.dequant_fused3d(lay_cpu["gu_blocks"][e:e + 1],
+                                        lay_cpu["gu_scales"][e:e + 1])[0]
+            wdn[e] = F3.dequant_fused3d(lay_cpu["dn_blocks"][e:e + 1],
+                                        lay_cpu["dn_scales"][e:e + 1])[0]
+        n_tok, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            t = n_tok % 8
+            F3.fused3d_experts(x[t:t + 1].cpu(), eidx[t:t + 1], w[t:t + 1].cpu(), **lay_cpu,
+                               w_gu=wgu, w_dn=wdn)
+            n_tok += 1
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(cpu_s * 1e6 / n_tok, 1), "unit": "us/token",
+               "cores": 1, "kind": "port",
+               "sample": f"{n_tok} tokens through the oracle (numpy float64, the 8 cycled "
+                         f"tokens' experts dequantized beforehand), {cpu_s:.1f} s"}
+        log(f"cpu baseline {cpu}")
+
+    result = {
+        "metric": "fused-3D MXFP4 MoE layer µs/token / MFMA util", "value": round(ms * 1000 / T, 4),
+        "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": spec["name"], "hidden": H, "experts": E, "inter": I,
+                   "top_k": K, "tokens": T, "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None,
+                     "kernels": "fused3d_gate_up + fused3d_down + prefill_reduce",
+                     "flops_per_call": flops, "weight_bytes": wbytes},
+        "parity": parity, "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def bench_gdn(args, spec):
     """A gated-delta mixer's decode step (conv update -> recurrent rule -> gated norm) for
     `mixers` x `copies` mixers with their own HBM-resident states, recorded in one graph."""
@@ -507,6 +626,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     spec = WORKLOADS[args.workload]
+    if spec is not None and spec.get("fused3d"):
+        bench_fused3d(args, spec)
+        return
     if spec is not None and spec.get("gdn"):
         bench_gdn(args, spec)
         return

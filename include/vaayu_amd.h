@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 4
+#define VAAYU_ABI_VERSION 5
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -199,6 +199,35 @@ int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
                          const int64_t *strides, int64_t rows, int32_t N, float eps,
                          int32_t x_dtype, int32_t z_dtype, int32_t w_dtype, int32_t round_mid,
                          void *stream);
+
+/* Routed fused-3D MXFP4 experts (gpt-oss layout), ABI 5. Replaces the vendored `matmul_ogs`
+ * calls with the fused `swiglu` that the experts module runs on the routed rows (caller:
+ * vaayu/routed_fused3d.py:131-238; vendor gpt_oss_triton_kernels matmul_ogs.py,
+ * matmul_ogs_details/_matmul_ogs.py:310-349, swiglu_details/_swiglu.py compute_swiglu).
+ * Weights are read in place from the layer's whole tensors: gate_up blocks
+ * [E, 2I, H/32, 16] (row 2j gate column j, row 2j+1 up column j) + E8M0 scales [E, 2I, H/32];
+ * down blocks [E, H, I/32, 16] + scales [E, H, I/32]. rows / n_blocks: the prefill block plan
+ * (16 row ids per block, row id = token * top_k + slot, -1 padding); tbl [n_blocks, 2]: the
+ * block's expert (codes address, scales address); btbl [n_blocks]: its fp32 bias address.
+ * codes_end / scales_end: the tensors' ends (reads past them return zeros). H, I multiples
+ * of 32; hidden_pad / inter_pad: multiples of 128 at least H / I, the row pitches of x and
+ * h, whose padding columns must hold zeros. */
+
+/* h [tokens * top_k, inter_pad] bf16 <- bf16(swiglu(x_row . W_gu^T + b)) per live row:
+ * gate clipped above at `limit`, up to [-limit, limit], s = gate / (1 + exp(-alpha gate)),
+ * h = fma(s, up, s). x [tokens, hidden_pad] bf16. */
+int vaayu_fused3d_gate_up(const void *x, const int64_t *rows, const int64_t *tbl,
+                          const int64_t *btbl, void *h, int32_t n_blocks, int32_t top_k,
+                          int32_t hidden, int32_t hidden_pad, int32_t inter, int32_t inter_pad,
+                          const void *codes_end, const void *scales_end, float alpha,
+                          float limit, void *stream);
+
+/* y [tokens * top_k, hidden] fp32 <- bf16((h_row . W_down^T + b) * gammas[row]) per live row;
+ * `vaayu_prefill_reduce` then sums each token's slots in ascending expert id. */
+int vaayu_fused3d_down(const void *h, const int64_t *rows, const int64_t *tbl,
+                       const int64_t *btbl, const float *gammas, float *y, int32_t n_blocks,
+                       int32_t top_k, int32_t hidden, int32_t inter, int32_t inter_pad,
+                       const void *codes_end, const void *scales_end, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,161 @@
+"""Routed fused-3D MXFP4 experts on MI355X: the gpt-oss experts module's two `matmul_ogs`
+calls (+ fused SwiGLU) as hand-written HIP grouped GEMMs over the layer's whole expert
+tensors, read in place.
+
+The reference delivers a fused-3D layer sparsely (vaayu/routed_fused3d.py:131-238): the
+routed experts' rows are copied into persistent `[num_experts, ...]` device buffers and
+the model's own experts forward runs over them, i.e. transformers' `Mxfp4GptOssExperts`
+calling the vendored `matmul_ogs` twice (gate/up with bias and the gpt-oss SwiGLU fused,
+then down with bias and the routing weights) and its finalize sum over each token's slots.
+`Fused3DExperts.forward` is that computation over the same buffers and the same routing:
+
+  vaayu_fused3d_gate_up  grouped gate/up GEMM on MFMA, bias + SwiGLU in the epilogue
+                         (gate clipped above at `limit`, up to [-limit, limit],
+                         s = gate * sigmoid(alpha gate), h = s * (up + 1)), h in bf16
+  vaayu_fused3d_down     grouped down GEMM, (acc + bias) * routing weight, rounded to bf16
+  vaayu_prefill_reduce   each token's slots summed in ascending expert id, in fp32
+
+Rows are planned as the packed-expert prefill plans them (16-row blocks of one expert,
+vaayu/packed_expert_kernels.py:676-717); the tensors' layout is the checkpoint's
+(`gate_up_proj_blocks` [E, 2I, H/32, 16] with gate / up rows interleaved, E8M0 scales
+[E, 2I, H/32], and the down pair), so nothing is repacked. Without the built library the
+forward raises ImportError; there is no CPU substitute.
+"""
+import torch
+
+from . import _lib
+from . import packed_expert_kernels as pk
+
+_BLOCK_M = pk._PF_BLOCK_M
+_STEP = 128                      # K codes per step of the kernels' K loop
+
+
+def _ceil(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+class Fused3DExperts:
+    """One layer's fused-3D MXFP4 experts. Tensors stay where they are (one device); the
+    biases are kept as fp32 copies (the experts module hands them to `matmul_ogs` as
+    `.to(torch.float32)`). `alpha` / `limit`: the gpt-oss SwiGLU's (1.702, 7.0 there)."""
+
+    def __init__(self, gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks, down_scales,
+                 down_bias, alpha: float = 1.702, limit: float = 7.0):
+        E, two_i, hg, sixteen = gate_up_blocks.shape
+        if sixteen != 16 or two_i % 2:
+            raise ValueError("gate_up blocks must be [E, 2I, H/32, 16]")
+        I, H = two_i // 2, hg * 32
+        want = {"gate_up_blocks": (gate_up_blocks, (E, 2 * I, H // 32, 16), torch.uint8),
+                "gate_up_scales": (gate_up_scales, (E, 2 * I, H // 32), torch.uint8),
+                "gate_up_bias": (gate_up_bias, (E, 2 * I), None),
+                "down_blocks": (down_blocks, (E, H, I // 32, 16), torch.uint8),
+                "down_scales": (down_scales, (E, H, I // 32), torch.uint8),
+                "down_bias": (down_bias, (E, H), None)}
+        dev = gate_up_blocks.device
+        for name, (t, shape, dtype) in want.items():
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} is {tuple(t.shape)}, expected {shape}")
+            if dtype is not None and t.dtype != dtype:
+                raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+            if not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous")
+            if t.device != dev:
+                raise ValueError(f"{name} is on {t.device}, not {dev}")
+        if I % 32:
+            raise ValueError("the intermediate size must be a multiple of 32")
+        self.E, self.H, self.I = E, H, I
+        self.Hp, self.Ip = _ceil(H, _STEP), _ceil(I, _STEP)
+        self.device = dev
+        self.alpha, self.limit = float(alpha), float(limit)
+        self.gu_codes, self.gu_scales = gate_up_blocks, gate_up_scales
+        self.dn_codes, self.dn_scales = down_blocks, down_scales
+        self.gu_bias = gate_up_bias.to(torch.float32).contiguous()
+        self.dn_bias = down_bias.to(torch.float32).contiguous()
+        # per-expert byte strides of each tensor
+        self._stride = {"gu_c": 2 * I * H // 2, "gu_s": 2 * I * H // 32, "dn_c": H * I // 2,
+                        "dn_s": H * I // 32, "gu_b": 2 * I * 4, "dn_b": H * 4}
+
+    def _end(self, t):
+        return t.data_ptr() + t.numel() * t.element_size()
+
+    def tables(self, expert_ids):
+        """The call's device tables from ONE pinned copy: (gate/up table, down table,
+        gate/up bias table, down bias table, rows, slot order, n_blocks)."""
+        eidx = expert_ids.to("cpu", torch.int64)
+        if eidx.numel() and (int(eidx.min()) < 0 or int(eidx.max()) >= self.E):
+            raise ValueError(f"expert ids must be in [0, {self.E})")
+        n, top_k = eidx.shape
+        order, live, counts = pk._prefill_plan(eidx)
+        nblk = (counts + _BLOCK_M - 1) // _BLOCK_M
+        blk_end = nblk.cumsum(0)
+        n_blocks = int(blk_end[-1])
+        owner = torch.repeat_interleave(torch.arange(live.numel()), counts)
+        first_row = counts.cumsum(0) - counts
+        dest = (((blk_end - nblk) * _BLOCK_M)[owner] + torch.arange(order.numel())
+                - first_row[owner])
+        rows = torch.full((n_blocks * _BLOCK_M,), -1, dtype=torch.int64)
+        rows[dest] = order
+        e_blk = torch.repeat_interleave(live, nblk)
+        st = self._stride
+        cols = [torch.stack([self.gu_codes.data_ptr() + e_blk * st["gu_c"],
+                             self.gu_scales.data_ptr() + e_blk * st["gu_s"]], 1).reshape(-1),
+                torch.stack([self.dn_codes.data_ptr() + e_blk * st["dn_c"],
+                             self.dn_scales.data_ptr() + e_blk * st["dn_s"]], 1).reshape(-1),
+                self.gu_bias.data_ptr() + e_blk * st["gu_b"],
+                self.dn_bias.data_ptr() + e_blk * st["dn_b"], rows]
+        slot_order = (torch.argsort(eidx, dim=1, stable=True)
+                      + (torch.arange(n) * top_k)[:, None]).reshape(-1)
+        dev = pk._PF_TABLES.put(torch.cat(cols + [slot_order]), self.device)
+        sizes = [c.numel() for c in cols] + [slot_order.numel()]
+        out, at = [], 0
+        for s in sizes:
+            out.append(dev[at:at + s])
+            at += s
+        return (*out, n_blocks)
+
+    def forward(self, x, expert_ids, routing_weights):
+        """x [tokens, H] bf16; expert_ids [tokens, top_k] (any device; read on the host);
+        routing_weights [tokens, top_k] on x's device (the `gammas`). Returns [tokens, H]
+        bf16: each token's slots summed in ascending expert id."""
+        lib = pk._require_backend()
+        if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.H:
+            raise ValueError(f"x must be a bf16 [tokens, {self.H}] tensor")
+        T, top_k = expert_ids.shape
+        if T != x.shape[0] or tuple(routing_weights.shape) != (T, top_k):
+            raise ValueError("x, expert_ids and routing_weights disagree on the call's shape")
+        out = torch.empty(T, self.H, dtype=torch.float32, device=x.device)
+        if T == 0:
+            return out.to(x.dtype)
+        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks = self.tables(expert_ids)
+        if self.Hp == self.H and x.is_contiguous():
+            xp = x
+        else:
+            xp = torch.zeros(T, self.Hp, dtype=x.dtype, device=x.device)
+            xp[:, :self.H] = x
+        h = (torch.empty if self.Ip == self.I else torch.zeros)(
+            T * top_k, self.Ip, dtype=x.dtype, device=x.device)
+        y = torch.empty(T * top_k, self.H, dtype=torch.float32, device=x.device)
+        gammas = routing_weights.reshape(-1).to(torch.float32).contiguous()
+        self.launch(xp, h, y, out, (gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks), gammas,
+                    top_k)
+        return out.to(x.dtype)
+
+    def launch(self, xp, h, y, out, tables, gammas, top_k) -> None:
+        """The three kernels on prepared buffers (what `forward` runs; allocates nothing, so
+        a caller can record it in a graph): xp [tokens, Hp] bf16 with zero padding columns,
+        h [tokens * top_k, Ip] bf16 with zero padding columns, y [tokens * top_k, H] fp32,
+        out [tokens, H] fp32, `tables` from `tables()`, gammas fp32 [tokens * top_k]."""
+        lib = pk._require_backend()
+        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks = tables
+        st = _lib.stream_ptr(xp.device)
+        rc = lib.vaayu_fused3d_gate_up(
+            xp.data_ptr(), rows.data_ptr(), gu_t.data_ptr(), gu_b.data_ptr(), h.data_ptr(),
+            n_blocks, top_k, self.H, self.Hp, self.I, self.Ip, self._end(self.gu_codes),
+            self._end(self.gu_scales), self.alpha, self.limit, st)
+        _lib.check(rc, "vaayu_fused3d_gate_up")
+        rc = lib.vaayu_fused3d_down(
+            h.data_ptr(), rows.data_ptr(), dn_t.data_ptr(), dn_b.data_ptr(), gammas.data_ptr(),
+            y.data_ptr(), n_blocks, top_k, self.H, self.I, self.Ip, self._end(self.dn_codes),
+            self._end(self.dn_scales), st)
+        _lib.check(rc, "vaayu_fused3d_down")
+        pk._reduce(y, order, out, top_k)
