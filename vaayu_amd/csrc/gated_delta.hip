@@ -52,15 +52,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ── the recurrent gated delta rule ─────────────────────────────────────────────────────
 //
-// One block owns the state slice [K, 64 values] of one (batch, value head) and walks T:
-// lane = value column, wave w = state rows [w*KW, w*KW + KW) held in registers. Per step
+// Per step of one (batch, value head):
 //   h *= exp(g);  delta = (v - sum_k h[k] * k[k]) * beta;  h += k[k] * delta;
 //   o = sum_k h[k] * q[k]
-// with q, k l2-normalised in fp32 (eps 1e-6) when asked and q scaled by `scale`. The sums
-// over K run per wave over its rows, then over the four waves in wave order.
+// with q, k l2-normalised in fp32 (eps 1e-6) when asked and q scaled by `scale`.
 
 constexpr int kGdnWaves = 4;
-constexpr int kGdnVT = 64;
 
 struct GdnRuleArgs {
   const void *q, *k, *v, *g, *beta, *h0;
@@ -72,19 +69,27 @@ struct GdnRuleArgs {
   int g_dt, beta_dt, l2, store_ht, has_h0;
 };
 
-// GB: g and beta read as fp32 and the activation dtype (the mixers' own dtypes) with no
-// dtype branch; other dtypes go through the generic reads.
-template <int ACT, int HDT, int KW, bool GB>
+// One workgroup per (batch, value head, 16 value columns): a (batch, head) spreads over
+// V/16 workgroups, since the kernel's time is load and store latency, not arithmetic (a
+// 64-column tile took 9.3 us against 6.7 for Qwen3-Next's decode shape). The fp32 state
+// slice stays in registers for every step: lane l of wave w holds column l & 15 and the
+// KW2 rows of k-group (w << 2) | (l >> 4). The sums over K add the lane's rows, then the
+// wave's four k-groups (lane ^ 16, lane ^ 32), then the four waves in wave order. GB: g
+// and beta read as fp32 and the activation dtype (the mixers' own) with no dtype branch.
+// Every load of a step is issued before its first wait, the first step's before the state.
+constexpr int kGdnVT = 16;
+
+template <int ACT, int HDT, int KW2, bool GB>
 __global__ void __launch_bounds__(kGdnWaves * 64) gdn_rule_kernel(GdnRuleArgs a) {
-  __shared__ float qs[kGdnWaves * KW], ks[kGdnWaves * KW];
+  constexpr int KMAX = 16 * KW2;
+  __shared__ float qs[KMAX], ks[KMAX];
   __shared__ float red[kGdnWaves][kGdnVT];
   __shared__ float nrm[2][kGdnWaves];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int vi = blockIdx.x * kGdnVT + lane;
+  const int col = lane & 15, kg = (w << 2) | (lane >> 4);
+  const int vi = blockIdx.x * kGdnVT + col;
   const int bh = blockIdx.y, b = bh / a.HV, hh = bh - b * a.HV;
   const bool vok = vi < a.V;
-  // The first step's operands are requested before the state, so the l2 norms can start
-  // while the state is still arriving; every load of a step is issued before its first wait.
   float qv = 0.f, kv = 0.f, vv = 0.f, graw = 0.f, beta = 0.f;
   auto load_step = [&](int t) {
     if (tid < a.K) {
@@ -105,14 +110,23 @@ __global__ void __launch_bounds__(kGdnWaves * 64) gdn_rule_kernel(GdnRuleArgs a)
     }
   };
   if (a.T > 0) load_step(0);
-  float h[KW];
+  float h[KW2];
 #pragma unroll
-  for (int i = 0; i < KW; ++i) {
-    const int kk = w * KW + i;
+  for (int i = 0; i < KW2; ++i) {
+    const int kk = kg * KW2 + i;
     h[i] = (a.has_h0 && vok && kk < a.K)
                ? load_as_float<HDT>(a.h0, b * a.sh[0] + hh * a.sh[1] + kk * a.sh[2] + vi * a.sh[3])
                : 0.f;
   }
+  auto sum_k = [&](float part) {                 // over the 16 k-groups, fixed order
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    if (lane < 16) red[w][lane] = part;
+    __syncthreads();
+    const float r = (red[0][col] + red[1][col]) + (red[2][col] + red[3][col]);
+    __syncthreads();
+    return r;
+  };
   for (int t = 0; t < a.T; ++t) {
     if (t > 0) load_step(t);
     if (a.l2) {
@@ -125,37 +139,31 @@ __global__ void __launch_bounds__(kGdnWaves * 64) gdn_rule_kernel(GdnRuleArgs a)
       kv = kv * rsqrtf(tk + 1e-6f);
     }
     qv = qv * a.scale;
-    if (tid < kGdnWaves * KW) { qs[tid] = qv; ks[tid] = kv; }     // rows past K hold 0
+    if (tid < KMAX) { qs[tid] = qv; ks[tid] = kv; }     // rows past K hold 0
     const float decay = expf(graw);
     __syncthreads();
     float part = 0.f;
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
+    for (int i = 0; i < KW2; ++i) {
       h[i] = h[i] * decay;
-      part += h[i] * ks[w * KW + i];
+      part += h[i] * ks[kg * KW2 + i];
     }
-    red[w][lane] = part;
-    __syncthreads();
-    const float kvm = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    const float kvm = sum_k(part);
     const float delta = (vv - kvm) * beta;
     float po = 0.f;
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-      h[i] = h[i] + ks[w * KW + i] * delta;
-      po += h[i] * qs[w * KW + i];
+    for (int i = 0; i < KW2; ++i) {
+      h[i] = h[i] + ks[kg * KW2 + i] * delta;
+      po += h[i] * qs[kg * KW2 + i];
     }
-    __syncthreads();                                   // every wave has read red
-    red[w][lane] = po;
-    __syncthreads();
-    if (w == 0 && vok)
-      store_act<ACT>(a.o, (((int64_t)b * a.T + t) * a.HV + hh) * a.V + vi,
-                     (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]));
-    __syncthreads();                                   // before the next step's writes
+    const float ov = sum_k(po);
+    if (tid < kGdnVT && vok)
+      store_act<ACT>(a.o, (((int64_t)b * a.T + t) * a.HV + hh) * a.V + vi, ov);
   }
   if (a.store_ht && vok) {
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-      const int kk = w * KW + i;
+    for (int i = 0; i < KW2; ++i) {
+      const int kk = kg * KW2 + i;
       if (kk < a.K) a.ht[((int64_t)bh * a.K + kk) * a.V + vi] = h[i];
     }
   }
@@ -312,14 +320,15 @@ extern "C" int vaayu_gdn_rule(const void* q, const void* k, const void* v, const
   a.g_dt = g_dtype; a.beta_dt = beta_dtype; a.l2 = l2norm != 0;
   a.store_ht = ht != nullptr; a.has_h0 = h0 != nullptr;
   const int hdt = h0 ? h0_dtype : DT_FP32;
-  const dim3 grid((unsigned)((V + kGdnVT - 1) / kGdnVT), (unsigned)(B * HV)), block(kGdnWaves * 64);
   hipStream_t st = (hipStream_t)stream;
   const bool gb = g_dtype == DT_FP32 && beta_dtype == act_dtype;
-#define GR(A_, H_, KW_)                                                                 \
+  const dim3 grid((unsigned)((V + kGdnVT - 1) / kGdnVT), (unsigned)(B * HV)),
+      block(kGdnWaves * 64);
+#define GR(A_, H_, KW_)                                                                    \
   if (gb) hipLaunchKernelGGL((gdn_rule_kernel<A_, H_, KW_, true>), grid, block, 0, st, a); \
   else hipLaunchKernelGGL((gdn_rule_kernel<A_, H_, KW_, false>), grid, block, 0, st, a)
 #define GR_KW(A_, H_) \
-  if (K <= 4 * 16) GR(A_, H_, 16); else if (K <= 4 * 32) GR(A_, H_, 32); else GR(A_, H_, 64)
+  if (K <= 16 * 4) GR(A_, H_, 4); else if (K <= 16 * 8) GR(A_, H_, 8); else GR(A_, H_, 16)
 #define GR_H(A_) \
   if (hdt == DT_BF16) { GR_KW(A_, DT_BF16); } else if (hdt == DT_FP16) { GR_KW(A_, DT_FP16); } \
   else { GR_KW(A_, DT_FP32); }

@@ -8,8 +8,8 @@ launches per mixer per token. Each seam here is one hand-written HIP kernel
 (vaayu_amd/csrc/gated_delta.hip, C ABI `vaayu_gdn_rule`, `vaayu_gdn_conv_update`,
 `vaayu_gdn_gated_norm`):
 
-  rule  one workgroup per (batch, value head, 64 value columns): the fp32 state slice
-        [K, 64] lives in registers (four waves x K/4 rows) for every step of the call.
+  rule  one workgroup per (batch, value head, 16 value columns): the fp32 state slice
+        [K, 16] lives in registers (16 k-groups of K/16 rows) for every step of the call.
   conv  one thread per (batch, channel): shift, append, depthwise dot, silu, in place.
   norm  one wave per row.
 
