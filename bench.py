@@ -150,8 +150,8 @@ WORKLOADS = {
     "qwen3-mxfp4-decode": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, MXFP4 "
                                     "e2m1 experts with E8M0 scales per 32", fmt="mxfp4"),
     "qwen3-decode-routed": dict(name="Qwen3-30B-A3B-shape MoE layer decode, 1 token, int4 g128 "
-                                     "fp16 scales, router matmul + softmax top-k + pair table on "
-                                     "the GPU in the same graph", fmt="int4", routed=True),
+                                     "fp16 scales, router product + softmax top-k + pair table "
+                                     "on the GPU in the same graph", fmt="int4", routed=True),
     "dsv3-prefill": dict(name="DeepSeek-V3-shape MoE layer prefill, 2048 tokens", hidden=7168,
                          inter=2048, experts=256, top_k=8, tokens=2048, routing="zipf",
                          shared=True, bound="mfma"),
@@ -725,18 +725,18 @@ def main():
     # ── routed: the router product, the routing and the pair table on the GPU too ───────
     routed_layer = None
     if spec is not None and spec.get("routed"):
-        from vaayu_amd.device_routing import ResidentExperts
+        from vaayu_amd.device_routing import ResidentExperts, router_logits
         rg = torch.Generator(device=dev).manual_seed(7)
         rxs = [ResidentExperts(layers[l]) for l in range(L)]
-        # the router's weight stored transposed ([hidden, experts], contiguous)
-        w_rt = [(torch.randn(H, E, generator=rg, device=dev) * 0.05).to(torch.bfloat16)
+        # the model's gate weight [experts, hidden]; its product runs as router_logits
+        w_rt = [(torch.randn(E, H, generator=rg, device=dev) * 0.05).to(torch.bfloat16)
                 for _ in range(L)]
         r_logits = [torch.empty(1, E, dtype=torch.bfloat16, device=dev) for _ in range(L)]
         r_bufs = [rx.buffers(K, x.dtype) for rx in rxs]
         r_outs = [torch.empty(1, H, dtype=torch.float32, device=dev) for _ in range(L)]
 
         def routed_layer(l, _stream):
-            torch.matmul(x, w_rt[l], out=r_logits[l])
+            router_logits(x, w_rt[l], out=r_logits[l])
             rxs[l].decode(x, r_logits[l], K, r_outs[l], bufs=r_bufs[l])
 
         for l in range(L):

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 5
+#define VAAYU_ABI_VERSION 6
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -159,6 +159,15 @@ int vaayu_route_topk(const void *logits, int32_t logits_dtype, int32_t tokens, i
                      int32_t top_k, int32_t keep_k, float top_p, int32_t renorm, float *weights,
                      int64_t *ids, const int64_t *expert_table, int64_t *pair_table,
                      void *stream);
+
+/* The router's product for decode-sized calls (ABI 6): logits [tokens, experts] <-
+ * round_out(x [tokens, hidden] . w [experts, hidden]^T), the fp32 sum rounded once, as the
+ * model's gate `F.linear(x, w)` stores it (the `router(flat_hidden)` call of `_route`,
+ * vaayu/moe_patch.py:2327). x and w bf16 (0) or fp16 (1), contiguous, 16-byte aligned,
+ * hidden a multiple of 8; out_dtype x's dtype or fp32 (2). */
+int vaayu_router_logits(const void *x, const void *w, int32_t x_dtype, void *logits,
+                        int32_t out_dtype, int32_t tokens, int32_t hidden, int32_t experts,
+                        void *stream);
 
 /* Gated-delta-net decode kernels (ABI 4). dtype codes 0 bf16, 1 fp16, 2 fp32. */
 

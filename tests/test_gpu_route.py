@@ -12,7 +12,7 @@ import torch
 
 import vaayu_amd.packed_expert_kernels as pk
 from vaayu_amd import _lib
-from vaayu_amd.device_routing import ResidentExperts, route_topk
+from vaayu_amd.device_routing import ResidentExperts, route_topk, router_logits
 from vaayu_amd.synth import random_expert
 from oracle import oracle as O
 
@@ -107,6 +107,41 @@ def test_the_budget_off_is_the_plain_routing():
     torch.cuda.synchronize()
     for other in (b, c):
         assert torch.equal(a[0], other[0]) and torch.equal(a[1], other[1])
+
+
+@pytest.mark.parametrize("tokens,hidden,experts,dtype,out_dtype", [
+    (1, 2048, 128, torch.bfloat16, None), (3, 7168, 256, torch.bfloat16, torch.float32),
+    (2, 1024, 32, torch.float16, None), (5, 4096, 8, torch.bfloat16, None)])
+def test_router_logits_are_the_correctly_rounded_product(tokens, hidden, experts, dtype,
+                                                         out_dtype):
+    """Against the fp64 product rounded once: within one unit in the last place of a 16-bit
+    output dtype (fp32 accumulation order) and mostly equal, within 2^-20 relative for fp32
+    outputs, and close to torch's own F.linear."""
+    g = torch.Generator().manual_seed(hidden + experts)
+    x = torch.randn(tokens, hidden, generator=g).to(dtype)
+    w = (torch.randn(experts, hidden, generator=g) * 0.02).to(dtype)
+    got = router_logits(x.to(DEV), w.to(DEV), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    exact = (x.double() @ w.double().T).numpy()
+    od = out_dtype or dtype
+    ref = O.round_to(exact, O.act_name(od))
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 2.0 ** -20}[od]
+    gv = O.to_np(got)
+    assert got.dtype == od
+    assert (np.abs(gv - ref) <= ulp * np.abs(ref) + 1e-6).all()
+    if od != torch.float32:                  # fp32 outputs carry the fp32 sum's own error
+        assert (gv == ref).mean() > 0.9
+    lib = torch.nn.functional.linear(x.to(DEV), w.to(DEV)).to(od)
+    assert O.rel_l2(gv, O.to_np(lib)) < 1e-2
+
+
+def test_router_logits_reject_bad_shapes():
+    with pytest.raises(ValueError):
+        router_logits(torch.zeros(1, 64, device=DEV, dtype=torch.bfloat16),
+                      torch.zeros(8, 32, device=DEV, dtype=torch.bfloat16))
+    with pytest.raises(_lib.KernelError):
+        router_logits(torch.zeros(1, 60, device=DEV, dtype=torch.bfloat16),
+                      torch.zeros(8, 60, device=DEV, dtype=torch.bfloat16))
 
 
 # ── the resident-expert decode ──────────────────────────────────────────────────────────
@@ -215,6 +250,35 @@ def test_one_graph_from_logits_to_the_sum_replays_exactly(layer):
         assert torch.equal(got_ids, bufs.ids), rep
         assert torch.equal(got_w, bufs.weights), rep
         assert torch.equal(got_out, out), rep
+
+
+def test_graph_with_the_router_product_on_the_gpu(layer):
+    """router_logits -> routing -> both kernels in one graph, replays equal to eager."""
+    blobs, rx = layer
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(1, H, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    w_router = (torch.randn(E, H, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    out = torch.empty(1, H, dtype=torch.float32, device=DEV)
+    bufs = rx.buffers(K, x.dtype)
+    logits = torch.empty(1, E, dtype=torch.bfloat16, device=DEV)
+
+    def layer_step():
+        router_logits(x, w_router, out=logits)
+        rx.decode(x, logits, K, out, bufs=bufs)
+
+    layer_step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer_step()
+    for rep in range(3):
+        x.copy_((torch.randn(1, H, generator=g) * 0.5).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_out, got_ids = out.clone(), bufs.ids.clone()
+        layer_step()
+        torch.cuda.synchronize()
+        assert torch.equal(got_ids, bufs.ids) and torch.equal(got_out, out), rep
 
 
 def test_resident_experts_reject_mixed_blobs(layer):

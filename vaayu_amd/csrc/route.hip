@@ -211,6 +211,43 @@ route_topk_kernel(const void* __restrict__ logits, int experts, int top_k, int k
   }
 }
 
+// The router's product for a few tokens: logits[t, e] = round_out(sum_h x[t, h] w[e, h]),
+// the fp32 sum rounded once to the output dtype, as `F.linear(x, w)` stores it. One wave
+// per (token, expert): 16-byte loads of x and of the expert's row, fp32 FMAs, a DPP wave
+// sum. For decode-sized calls, where a library GEMM's launch and tiling dominate.
+constexpr int kGemvWaves = 4;
+
+template <int XDT, int ODT>
+__global__ void __launch_bounds__(kGemvWaves * 64)
+router_gemv_kernel(const void* __restrict__ x, const void* __restrict__ w, void* __restrict__ out,
+                   int tokens, int hidden, int experts) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+  if (row >= (int64_t)tokens * experts) return;          // wave-uniform
+  const int t = (int)(row / experts), e = (int)(row - (int64_t)t * experts);
+  const uint16_t* xr = (const uint16_t*)x + (int64_t)t * hidden;
+  const uint16_t* wr = (const uint16_t*)w + (int64_t)e * hidden;
+  float acc = 0.f;
+  for (int k = lane * 8; k < hidden; k += 64 * 8) {       // hidden % 8 == 0
+    const uint4 xv = *(const uint4*)(xr + k);
+    const uint4 wv = *(const uint4*)(wr + k);
+    const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = load_as_float<XDT>(&xa[j], 0), x1 = load_as_float<XDT>(&xa[j], 1);
+      const float w0 = load_as_float<XDT>(&wa[j], 0), w1 = load_as_float<XDT>(&wa[j], 1);
+      acc = fmaf(x0, w0, acc);
+      acc = fmaf(x1, w1, acc);
+    }
+  }
+  acc = route_op<false>(acc, route_dpp<0xB1>(acc));
+  acc = route_op<false>(acc, route_dpp<0x4E>(acc));
+  acc = route_op<false>(acc, route_dpp<0x124>(acc));
+  acc = route_op<false>(acc, route_dpp<0x128>(acc));
+  acc = (route_lane(acc, 0) + route_lane(acc, 16)) + (route_lane(acc, 32) + route_lane(acc, 48));
+  if (lane == 0) store_act<ODT>(out, row, acc);
+}
+
 }  // namespace vaayu
 
 using namespace vaayu;
@@ -244,3 +281,31 @@ extern "C" int vaayu_route_topk(const void* logits, int32_t logits_dtype, int32_
 #undef RT
   return check_launch("route top-k");
 }
+
+extern "C" int vaayu_router_logits(const void* x, const void* w, int32_t x_dtype, void* logits,
+                                   int32_t out_dtype, int32_t tokens, int32_t hidden,
+                                   int32_t experts, void* stream) {
+  clear_error();
+  if (!x || !w || !logits) return set_error(-1, "null pointer argument");
+  if (tokens <= 0 || experts <= 0 || hidden <= 0) return set_error(-2, "empty shape");
+  if (hidden % 8) return set_error(-2, "hidden must be a multiple of 8");
+  if (x_dtype != DT_BF16 && x_dtype != DT_FP16)
+    return set_error(-2, "x and the router weight must be bf16 (0) or fp16 (1)");
+  if (out_dtype != x_dtype && out_dtype != DT_FP32)
+    return set_error(-2, "logits must be x's dtype or fp32 (2)");
+  if ((uintptr_t)x % 16 || (uintptr_t)w % 16) return set_error(-2, "x and w must be 16-byte aligned");
+  const int64_t rows = (int64_t)tokens * experts;
+  if ((rows + kGemvWaves - 1) / kGemvWaves > 0x7FFFFFFF) return set_error(-2, "too many rows");
+  const dim3 grid((unsigned)((rows + kGemvWaves - 1) / kGemvWaves)), block(kGemvWaves * 64);
+  hipStream_t st = (hipStream_t)stream;
+#define RG(X_, O_) hipLaunchKernelGGL((router_gemv_kernel<X_, O_>), grid, block, 0, st, x, w, logits, \
+                                      tokens, hidden, experts)
+  if (x_dtype == DT_BF16) {
+    if (out_dtype == DT_FP32) RG(DT_BF16, DT_FP32); else RG(DT_BF16, DT_BF16);
+  } else {
+    if (out_dtype == DT_FP32) RG(DT_FP16, DT_FP32); else RG(DT_FP16, DT_FP16);
+  }
+#undef RG
+  return check_launch("router logits");
+}
+

@@ -17,6 +17,26 @@ from . import _lib
 from . import packed_expert_kernels as pk
 
 
+def router_logits(x, weight, out=None, out_dtype=None):
+    """The model's gate product `F.linear(x, weight)` for decode-sized calls in one HIP
+    launch (one wave per token x expert, fp32 sum rounded once): x [tokens, hidden] and
+    weight [experts, hidden] bf16 or fp16, contiguous. Returns logits [tokens, experts] in
+    `out_dtype` (x's dtype by default, or fp32); `out` given: written in place."""
+    lib = pk._require_backend()
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError("x [tokens, hidden] and weight [experts, hidden] disagree")
+    if weight.dtype != x.dtype or not (x.is_contiguous() and weight.is_contiguous()):
+        raise ValueError("x and weight must be contiguous and of one dtype")
+    tokens, experts = x.shape[0], weight.shape[0]
+    if out is None:
+        out = torch.empty(tokens, experts, dtype=out_dtype or x.dtype, device=x.device)
+    rc = lib.vaayu_router_logits(x.data_ptr(), weight.data_ptr(), pk._DTYPE_CODE[x.dtype],
+                                 out.data_ptr(), pk._DTYPE_CODE[out.dtype], tokens, x.shape[1],
+                                 experts, _lib.stream_ptr(x.device))
+    _lib.check(rc, "vaayu_router_logits")
+    return out
+
+
 def _budget(top_k: int, keep_k, top_p):
     """(n_out, keep_k, top_p) for the C-ABI: `truncate_top_k`'s (k, p), None meaning off."""
     if keep_k is not None and keep_k < 1:
