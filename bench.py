@@ -34,7 +34,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--layers", type=int, default=48)
+    p.add_argument("--layers", type=int, default=None,
+                   help="resident layers per step (default 48; 8 Mixtral, 6 DeepSeek-V3)")
     p.add_argument("--distinct", type=int, default=2,
                    help="distinct random layers; the rest are byte copies at new addresses")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -56,7 +57,9 @@ def parse():
 # WRITE_SIZE of a dispatch are scaled by (256 MiB / what the counter reads for that
 # calibration dispatch), which turns the counters into HBM bytes.
 CALIB_BYTES = 256 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_qwen3_b1_traffic.txt")
+TRAFFIC_FILES = {"qwen3-decode": "decode_qwen3_b1_traffic.txt",
+                 "mixtral-decode": "decode_mixtral_b1_traffic.txt",
+                 "dsv3-decode": "decode_dsv3_b1_traffic.txt"}
 GU_KERNEL = "mfma_gate_up_kernel"     # the decode gate/up kernel bf16 activations run
 
 
@@ -113,18 +116,19 @@ def summarize(dirs):
     return "\n".join(out)
 
 
-def traffic_from_profile():
-    """HBM bytes per gate/up launch (FETCH_SIZE + WRITE_SIZE, scaled) from the committed
-    counter summary of this workload, or None."""
-    if not os.path.exists(TRAFFIC_FILE):
+def traffic_from_profile(workload, launches=1):
+    """HBM bytes of `launches` gate/up launches (FETCH_SIZE + WRITE_SIZE per launch, scaled)
+    from the committed counter summary of this workload, or None."""
+    path = os.path.join(ROOT, "profiles", TRAFFIC_FILES.get(workload, "-"))
+    if not os.path.exists(path):
         return None
     total, seen = 0.0, set()
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         f = line.split()
         if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == GU_KERNEL:
             total += float(f[3])
             seen.add(f[2])
-    return round(total) if seen == {"FETCH_SIZE", "WRITE_SIZE"} else None
+    return round(total * launches) if seen == {"FETCH_SIZE", "WRITE_SIZE"} else None
 
 
 def log(msg):
@@ -166,6 +170,13 @@ WORKLOADS = {
                                     "tokens (32 experts, hidden 2880, inter 2880, top-4)",
                                fused3d=True, hidden=2880, inter=2880, experts=32, top_k=4,
                                tokens=2048),
+    "mixtral-decode": dict(name="Mixtral-8x7B-shape MoE layer decode, 1 token, int4 g128 fp16 "
+                                "scales", fmt="int4", decode_shape=dict(hidden=4096, inter=14336,
+                                experts=8, top_k=2, layers=8, shared=False)),
+    "dsv3-decode": dict(name="DeepSeek-V3-shape MoE layer decode, 1 token, int4 g128 fp16 "
+                             "scales, 8 of 256 routed experts + 1 shared expert", fmt="int4",
+                        decode_shape=dict(hidden=7168, inter=2048, experts=256, top_k=8,
+                                          layers=6, shared=True)),
     "qwen3-decode-b8": dict(name="Qwen3-30B-A3B-shape MoE layer decode, batch of 8 tokens",
                             hidden=2048, inter=768, experts=128, top_k=8, tokens=8,
                             routing="softmax", shared=False, bound="hbm"),
@@ -647,8 +658,14 @@ def main():
     lib = _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    H, E, I, K, BITS, GS = 2048, 128, 768, 8, 4, 128
-    L = args.layers
+    shape = dict(hidden=2048, inter=768, experts=128, top_k=8, layers=48, shared=False)
+    if spec is not None:
+        shape.update(spec.get("decode_shape", {}))
+    H, E, I, K, BITS, GS = (shape["hidden"], shape["experts"], shape["inter"], shape["top_k"],
+                            4, 128)
+    L = args.layers or shape["layers"]
+    SHARED = shape["shared"]
+    n_exp = E + (1 if SHARED else 0)        # the shared expert is blob E of a layer
 
     # ── experts: `distinct` random layers, the rest byte copies at fresh addresses ─────
     t0 = time.time()
@@ -658,12 +675,12 @@ def main():
                                      scale_dtype=torch.float16)
     else:
         make = lambda: random_format_expert(fmt, H, I, generator=gen, device=dev, std=0.02)
-    base = [[make() for _ in range(E)] for _ in range(min(args.distinct, L))]
+    base = [[make() for _ in range(n_exp)] for _ in range(min(args.distinct, L))]
     layers = [base[l] if l < len(base) else [clone_blob(b) for b in base[l % len(base)]]
               for l in range(L)]
     torch.cuda.synchronize()
     per_expert = sum(t.numel() * t.element_size() for t in layers[0][0]["flat"].values())
-    log(f"{L} layers x {E} experts resident: {L * E * per_expert / 1e9:.2f} GB "
+    log(f"{L} layers x {n_exp} experts resident: {L * n_exp * per_expert / 1e9:.2f} GB "
         f"({time.time() - t0:.1f} s)")
     geom = layers[0][0]["geom"]
     sc = pk._SCALE_CODE[layers[0][0]["flat"]["scale"].dtype]
@@ -684,14 +701,32 @@ def main():
         rws.append(w.to(dev))
         hs.append(torch.empty(K, I, dtype=torch.bfloat16, device=dev))
         outs.append(torch.empty(1, H, dtype=torch.float32, device=dev))
+    # DeepSeek's always-on shared expert: a one-slot call of weight 1 per layer (the
+    # engine adds its output after the routed sum is cast to bf16; that add is not timed)
+    sh = []
+    if SHARED:
+        one = torch.ones(1, 1, dtype=torch.float32, device=dev)
+        for l in range(L):
+            sh.append((torch.tensor(pk._table_values([(layers[l][E], 0)]), dtype=torch.int64,
+                                    device=dev),
+                       torch.empty(1, I, dtype=torch.bfloat16, device=dev),
+                       torch.empty(1, H, dtype=torch.float32, device=dev)))
 
     def gate_up(l, stream):
-        return lib.vaayu_decode_gate_up(x.data_ptr(), tables[l].data_ptr(), hs[l].data_ptr(),
-                                        K, g, 0, sc, stream)
+        rc = lib.vaayu_decode_gate_up(x.data_ptr(), tables[l].data_ptr(), hs[l].data_ptr(),
+                                      K, g, 0, sc, stream)
+        if SHARED and rc == 0:
+            rc = lib.vaayu_decode_gate_up(x.data_ptr(), sh[l][0].data_ptr(), sh[l][1].data_ptr(),
+                                          1, g, 0, sc, stream)
+        return rc
 
     def down(l, stream):
-        return lib.vaayu_decode_down(hs[l].data_ptr(), tables[l].data_ptr(), rws[l].data_ptr(),
-                                     2, outs[l].data_ptr(), K, g, 0, sc, 0, stream)
+        rc = lib.vaayu_decode_down(hs[l].data_ptr(), tables[l].data_ptr(), rws[l].data_ptr(),
+                                   2, outs[l].data_ptr(), K, g, 0, sc, 0, stream)
+        if SHARED and rc == 0:
+            rc = lib.vaayu_decode_down(sh[l][1].data_ptr(), sh[l][0].data_ptr(), one.data_ptr(),
+                                       2, sh[l][2].data_ptr(), 1, g, 0, sc, 0, stream)
+        return rc
 
     def capture(body):
         graph = torch.cuda.CUDAGraph()
@@ -761,7 +796,7 @@ def main():
     ms_dn = time_graph(dn_only, args.steps, args.warmup)
     us_tok_layer = ms_step * 1000.0 / L
     log(f"step {ms_step:.3f} ms = {us_tok_layer:.2f} us/token/layer; gate_up "
-        f"{ms_gu * 1000 / L:.2f} us, down {ms_dn * 1000 / L:.2f} us per launch")
+        f"{ms_gu * 1000 / L:.2f} us, down {ms_dn * 1000 / L:.2f} us per layer")
     routed_extra = None
     if routed_layer is not None:
         ms_routed = time_graph(routed_graph, args.steps, args.warmup)
@@ -779,8 +814,10 @@ def main():
     def role_bytes(rows, cols):             # codes + scales of one role
         return rows * cols * bits // 8 + (rows // brows) * (cols // group) * sc_el
 
-    gu_bytes = K * 2 * role_bytes(I, H) + H * 2 + K * I * 2
-    dn_bytes = K * role_bytes(H, I) + K * I * 2 + H * 4
+    NX = K + (1 if SHARED else 0)             # expert blobs one token reads per layer
+    NL = 2 if SHARED else 1                   # launches of each kernel per layer
+    gu_bytes = NX * 2 * role_bytes(I, H) + H * 2 * (2 if SHARED else 1) + NX * I * 2
+    dn_bytes = NX * role_bytes(H, I) + NX * I * 2 + H * 4 * (2 if SHARED else 1)
     gu_gbs = gu_bytes / (ms_gu * 1e-3 / L) / 1e9
     dn_gbs = dn_bytes / (ms_dn * 1e-3 / L) / 1e9
     layer_gbs = (gu_bytes + dn_bytes) / (us_tok_layer * 1e-6) / 1e9
@@ -790,10 +827,28 @@ def main():
     ids, order, w = routed[0]
     cpu_pairs = [({"flat": {n: t.cpu() for n, t in layers[0][ids[s]]["flat"].items()},
                    "geom": geom}, s) for s in order]
-    ref = O.stock_decode(x.cpu(), cpu_pairs, w)
+    # the numpy restatement takes minutes per call at Mixtral's expert size; its torch
+    # port of the stock loop (pinned against it in the oracle's tests) checks those shapes
+    big = H * I > 4e6
+
+    def stock(xc, pairs, wc):
+        if not big:
+            return O.stock_decode(xc, pairs, wc)
+        o = torch.empty(1, H)
+        O.stock_decode_torch(xc, pairs, wc, o)
+        return o.numpy()
+
+    ref = stock(x.cpu(), cpu_pairs, w)
     got = outs[0].cpu().numpy()
     parity = {"relL2": O.rel_l2(got, ref), "max_abs": float(np.abs(got - ref).max()),
               "tolerance": {"relL2": 5e-3, "max_abs": 2e-2}}
+    if SHARED:
+        sref = stock(x.cpu(), [({"flat": {n: t.cpu() for n, t in
+                                                   layers[0][E]["flat"].items()},
+                                          "geom": geom}, 0)], torch.ones(1, 1))
+        sgot = sh[0][2].cpu().numpy()
+        parity["shared"] = {"relL2": O.rel_l2(sgot, sref),
+                            "max_abs": float(np.abs(sgot - sref).max())}
     if routed_layer is not None:             # layer 0 as routed on the GPU
         want_w, want_ids = O.route_softmax_topk(r_logits[0].cpu().float(), K)
         got_ids, got_w = r_bufs[0].ids.cpu().numpy(), r_bufs[0].weights.cpu()
@@ -820,20 +875,29 @@ def main():
             samples.append(([({"flat": {n: t.cpu() for n, t in layers[l][ids[s]]["flat"].items()},
                                "geom": geom}, s) for s in order], w))
         out = torch.empty(1, H)
+        s_pair = ([({"flat": {n: t.cpu() for n, t in layers[0][E]["flat"].items()},
+                     "geom": geom}, 0)] if SHARED else None)
+        s_out, s_w = torch.empty(1, H), torch.ones(1, 1)
         O.stock_decode_torch(xc, samples[0][0], samples[0][1], out)     # warm
         n_calls, t_start = 0, time.perf_counter()
-        while time.perf_counter() - t_start < args.cpu_seconds:
+        while time.perf_counter() - t_start < args.cpu_seconds or n_calls == 0:
             pairs, w = samples[n_calls % len(samples)]
             O.stock_decode_torch(xc, pairs, w, out)
+            if s_pair is not None:
+                O.stock_decode_torch(xc, s_pair, s_w, s_out)
             n_calls += 1
         cpu_s = time.perf_counter() - t_start
         cpu = {"value": cpu_s * 1e6 / n_calls, "unit": "us/token per MoE layer",
                "cores": threads, "kind": "port",
                "sample": f"{n_calls} one-token decodes of the same layer shape (8 layers' routed "
-                         f"experts copied to host, cycled), torch CPU bf16 stock loop, "
+                         f"experts{' and the shared expert' if SHARED else ''} copied to host, "
+                         f"cycled), torch CPU bf16 stock loop, "
                          f"{cpu_s:.1f} s"}
         log(f"cpu baseline {cpu}")
 
+    # a layer with the shared expert runs each kernel twice (routed, shared): its figures
+    # are per layer, i.e. per pair of launches
+    per, unit = ("", "launch") if NL == 1 else ("routed_and_shared_", "layer")
     result = {
         "metric": METRIC, "value": round(us_tok_layer, 3), "unit": "us/token",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -843,17 +907,17 @@ def main():
                                 "Qwen3-30B-A3B-shape MoE layer decode, 1 token, int4 g128 fp16 "
                                 "scales") + f", {L} HBM-resident layers per step",
                    "hidden": H, "experts": E, "inter": I, "top_k": K, "layers": L,
-                   "tokens": 1, "parallelism": "none (one GPU)"},
+                   "shared_expert": SHARED, "tokens": 1, "parallelism": "none (one GPU)"},
         "tokens_per_s_per_layer": round(1e6 / us_tok_layer, 1),
         "layer_hbm_gbs": round(layer_gbs, 1),
         "roofline": {"bound": "hbm", "kernel": GU_KERNEL,
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile() if fmt == "int4" else None,
-                     "bytes_per_launch": gu_bytes,
-                     "us_per_launch": round(ms_gu * 1000 / L, 3)},
-        "down_kernel": {"achieved_gbs": round(dn_gbs, 1), "bytes_per_launch": dn_bytes,
-                        "us_per_launch": round(ms_dn * 1000 / L, 3)},
+                     "traffic": traffic_from_profile(args.workload, NL),
+                     per + "bytes_per_" + unit: gu_bytes,
+                     per + "us_per_" + unit: round(ms_gu * 1000 / L, 3)},
+        "down_kernel": {"achieved_gbs": round(dn_gbs, 1), per + "bytes_per_" + unit: dn_bytes,
+                        per + "us_per_" + unit: round(ms_dn * 1000 / L, 3)},
         "parity": parity,
         "cpu_baseline": cpu,
     }

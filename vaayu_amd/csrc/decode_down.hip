@@ -50,8 +50,12 @@ static int mfma_down_sw(const void* h, const int64_t* tbl, const void* rw, int r
 
 // The MFMA kernel's plan for this launch, or false when it does not take it. K parts: the
 // most of 4, 2, 1 that split the intermediate dimension into whole steps (4 units each).
-// Row groups per wave (nrg) keep the grid near 512 blocks at most, since every block stages
-// all pairs' h.
+// Row groups per wave (nrg) keep the grid at kMaxDownBlocks blocks at most, since every
+// block stages all pairs' h. A wave starts a row group's requests only when the previous
+// one is done, so each extra row group exposes a full memory latency; up to 2048 blocks
+// (h re-read from L2 per block) the straight one-group kernel is the faster trade.
+constexpr int64_t kMaxDownBlocks = 2048;
+
 static bool mfma_down_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, DownPlan& d) {
   if (!mfma_format(fmt, act)) return false;
   const int cpu = 128 / (fmt % 100);
@@ -67,7 +71,7 @@ static bool mfma_down_plan(const vaayu_geom* g, int fmt, int act, int n, int sc,
   while (d.ps < 8 && d.ps < n) d.ps <<= 1;
   const int rows_g = (8 / d.ps) * (16 / d.kp);               // rows per block per row group
   const int64_t blocks1 = (g->hidden + rows_g - 1) / rows_g;
-  d.nrg = (int)std::max<int64_t>(1, (blocks1 + 511) / 512);
+  d.nrg = (int)std::max<int64_t>(1, (blocks1 + kMaxDownBlocks - 1) / kMaxDownBlocks);
   const int br = d.nrg * rows_g;
   d.blocks = (unsigned)((g->hidden + br - 1) / br);
   d.lds = (size_t)vec16 * 16 + (size_t)n * br * sizeof(float);
