@@ -36,6 +36,14 @@ __device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t byte_off) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// The same load marked non-temporal (the cache-policy nt bit): for expert codes read once
+// per call, so their lines are the first to leave L2 and the small operands the next
+// kernels need (pointer tables, activations) stay cached.
+__device__ __forceinline__ uint4 buf_load16_nt(rsrc_t r, uint32_t byte_off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 2);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // A scale of SW bits (8: E8M0, 16: bf16 / fp16, 32: fp32), raw (converted only where it is used,
 // so the load is not waited for early).
 template <int SW>

@@ -81,8 +81,8 @@ struct MShape {
 // reads past the part, within the buffer or as zeros, and does not use it).
 // cbase / sbase: byte offset of the lane's first unit and element index of its row's first
 // scale; u0 its first unit's index in the row (for the scale group); `xa` the lane's A
-// operands (read where a_lane).
-template <int F, int ACT, int SW, int NS>
+// operands (read where a_lane). NT: the codes are requested non-temporal.
+template <int F, int ACT, int SW, int NS, bool NT = true>
 struct ColumnDot {
   static constexpr int NMF = MUnit<F>::NMF;
   static constexpr int NB = NS > 0 ? NS : 4;       // steps per register chunk
@@ -98,7 +98,8 @@ struct ColumnDot {
   __device__ __forceinline__ void load(uint4 (&qv)[NB], uint32_t (&sv)[NB], int st0) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      qv[i] = buf_load16(P, cbase + (uint32_t)(st0 + i) * 64u);
+      qv[i] = NT ? buf_load16_nt(P, cbase + (uint32_t)(st0 + i) * 64u)
+                 : buf_load16(P, cbase + (uint32_t)(st0 + i) * 64u);
       sv[i] = buf_load_scale<SW>(S, sbase + ((u0 + 4u * (uint32_t)(st0 + i)) >> ushift));
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -161,7 +162,7 @@ struct ColumnDot {
 // LDS-only barrier while the codes stream. The four parts of a column
 // are summed with two row rotations, the up total is fetched beside the gate total with a
 // quad exchange, and lanes 0 and 1 write h.
-template <int F, int ACT, int SW, int NS>
+template <int F, int ACT, int SW, int NS, bool NT>
 __global__ void __launch_bounds__(256)
 mfma_gate_up_kernel(const int64_t* __restrict__ tbl, const uint32_t* __restrict__ x,
                     void* __restrict__ h, MShape s) {
@@ -187,7 +188,7 @@ mfma_gate_up_kernel(const int64_t* __restrict__ tbl, const uint32_t* __restrict_
   const uint32_t u0 = (uint32_t)(kp * s.part_units + q);
   const uint32_t cbase = (role ? s.wb1 : s.wb0) + ((uint32_t)row * s.units_row + u0) * 16u;
   const uint32_t sbase = (role ? s.sc1 : s.sc0) + (uint32_t)(row >> s.rshift) * s.groups_row;
-  ColumnDot<F, ACT, SW, NS> cd;
+  ColumnDot<F, ACT, SW, NS, NT> cd;
   cd.begin(P, S, cbase, sbase, u0, s);
 #pragma unroll
   for (int k = 0; k < 4; ++k)
@@ -241,7 +242,7 @@ mfma_down_kernel(const int64_t* __restrict__ tbl, const void* __restrict__ h,
   const int p16 = s.units_row * CPU / 8;                     // uint4 of one pair's h
   float* cbuf = (float*)(lds + s.vec16);
   const uint32_t u0 = (uint32_t)(kp * s.part_units + q);
-  ColumnDot<F, ACT, SW, NS> cd;
+  ColumnDot<F, ACT, SW, NS> cd;     // codes non-temporal: no shape measured slower with it
   // the operands of (row group 0, pair pl) go out before the staging barrier (an idle wave,
   // pl >= n_pairs, loads pair 0's and does not use them)
   auto begin = [&](int gi, int p) {
