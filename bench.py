@@ -294,7 +294,11 @@ def bench_prefill(args, spec):
         return a.elapsed_time(b) / steps
 
     steps = max(1, args.steps // (5 if T >= 512 else 1))
-    stage_ms = {st: time_graph(capture(lambda st=st: run_stage(st)), steps, args.warmup)
+    # each stage ten times in one graph: a graph of one short kernel replays at the host's
+    # launch rate, not the GPU's (the stages are idempotent)
+    rep = 10
+    stage_ms = {st: time_graph(capture(lambda st=st: [run_stage(st) for _ in range(rep)]),
+                               steps, args.warmup) / rep
                 for st in ("gate_up", "down", "reduce")}
     ms = time_graph(capture(run_layer), steps, args.warmup)
     flops = 2 * T * K * 3 * H * I + (2 * T * 3 * H * I if spec["shared"] else 0)

@@ -96,6 +96,24 @@ def test_the_token_sum_runs_in_expert_id_order(hid, inter, bits, gs):
     assert np.array_equal(O.to_np(out), want)
 
 
+@pytest.mark.parametrize("tokens,top_k", [(3, 10), (8, 8), (5, 17), (600, 10)],
+                         ids=["few-tokens-k10", "b8-k8", "few-tokens-k17", "many-tokens-k10"])
+def test_the_token_sum_is_exact_for_any_slot_count(tokens, top_k):
+    """The reduce alone, on small and large grids and top_k above eight: bit-equal to the
+    sequential sum in `ord` order, values spread over many binades so order matters."""
+    hid = 1024
+    g = torch.Generator().manual_seed(tokens * 31 + top_k)
+    y = (torch.randn(tokens * top_k, hid, generator=g)
+         * torch.exp2(torch.randint(-20, 20, (tokens * top_k, 1), generator=g).float()))
+    order = torch.stack([torch.randperm(tokens * top_k, generator=g)[:top_k]
+                         for _ in range(tokens)])
+    out = torch.full((tokens, hid), float("nan"), device="cuda")
+    pk._reduce(y.cuda(), order.cuda(), out, top_k)
+    torch.cuda.synchronize()
+    want = O.reduce_in_order(y.numpy(), order.numpy(), tokens, top_k)
+    assert np.array_equal(O.to_np(out), want)
+
+
 @pytest.mark.parametrize("hid,inter,bits,gs", GEOMS)
 def test_kernel_output_is_as_accurate_as_the_stock_arithmetic(hid, inter, bits, gs):
     x, eidx, w, blobs, cblobs = prefill_case(hid, inter, bits, gs)
