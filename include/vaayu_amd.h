@@ -58,8 +58,9 @@ typedef struct vaayu_geom {
 int vaayu_abi_version(void);
 const char *vaayu_last_error(void);
 
-/* The decode entries take every code format above, scale_dtype 0 bf16, 1 fp16, 2 fp32 or
- * 3 E8M0; the prefill entries take VAAYU_FMT_INT. */
+/* The decode and prefill entries take every code format above (prefill: 4- and 8-bit
+ * codes, bf16 / fp16 activations), scale_dtype 0 bf16, 1 fp16, 2 fp32 or 3 E8M0 (E8M0 with
+ * VAAYU_FMT_MXFP4 only). */
 
 /* Decode, gate/up stage. Replaces `_gate_up` / `_gate_up_kernel`
  * (vaayu/packed_expert_kernels.py:355-371, 131-150).
@@ -84,7 +85,10 @@ int vaayu_decode_down(const void *h, const int64_t *table, const void *routing_w
  * x     [tokens, hidden] contiguous (dtype `act`: bf16 or fp16)
  * rows  int64 [n_blocks * 16]: row ids token*top_k + slot, -1 pads a block
  * table int64 [n_blocks * 2]: (packed address, scale address) of each block's expert
- * h     [tokens * top_k, inter] (dtype `act`); padding rows are never written */
+ * h     [tokens * top_k, inter] (dtype `act`); padding rows are never written
+ * x and h rows are addressed with 32-bit byte offsets: a launch whose tables could hold
+ * rows past 0xF0000000 bytes (n_blocks * 16 / top_k tokens of x) is refused with -2; split
+ * such a call into token chunks (every row's arithmetic is independent of its launch-mates). */
 int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *table, void *h,
                           int32_t n_blocks, int32_t top_k, const vaayu_geom *geom, int32_t act,
                           int32_t scale_dtype, void *stream);
@@ -92,7 +96,8 @@ int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *tab
 /* Prefill, down stage. Replaces `_down_g` / `_down_grouped`
  * (vaayu/packed_expert_kernels.py:735-749, 218-247).
  * y [tokens * top_k, hidden] fp32 <- fl32(round(h[row].Wd) * routing_weights[row]),
- * rounded again when w_round != 0; routing_weights contiguous [tokens * top_k]. */
+ * rounded again when w_round != 0; routing_weights contiguous [tokens * top_k].
+ * Refused with -2 when n_blocks * 16 rows of h would reach past 0xF0000000 bytes. */
 int vaayu_prefill_down(const void *h, const int64_t *rows, const int64_t *table,
                        const void *routing_weights, int32_t rw_dtype, float *y,
                        int32_t n_blocks, const vaayu_geom *geom, int32_t act,
@@ -106,7 +111,8 @@ int vaayu_prefill_reduce(const float *y, const int64_t *order, float *out, int32
 
 /* Whole-blob dequant. Replaces `_fused_dequant_kernel` (vaayu/moe_patch.py:750-769), the
  * function `dequantize_expert_blob` (:849-868) runs: out[i] = round_out((code_i -
- * 2^(bits-1)) * round_out(scale[i / group])) over n_words * 32/bits codes, bit-exact. */
+ * 2^(bits-1)) * round_out(scale[i / group])) over n_words * 32/bits codes, bit-exact.
+ * packed and out must start on 16 bytes (-2 otherwise). */
 int vaayu_dequant_blob(const int32_t *packed, const void *scale, int32_t scale_dtype, void *out,
                        int32_t out_dtype, int64_t n_words, int32_t bits, int32_t group,
                        void *stream);

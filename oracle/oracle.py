@@ -234,8 +234,12 @@ def dequant_flat(flat_packed, flat_scale, num_bits: int, group_size: int, act) -
     per = 32 // num_bits
     shifts = (np.arange(per, dtype=np.uint32) * np.uint32(num_bits))
     codes = (p[:, None] >> shifts[None, :]) & np.uint32((1 << num_bits) - 1)
-    codes = codes.reshape(-1, group_size).astype(np.float64) - (1 << (num_bits - 1))
-    s = round_to(to_np(flat_scale).astype(np.float32), act).astype(np.float64)
+    # The product (c - off) * s is exact in float32 when s has at most 11 significant bits
+    # (a bf16 / fp16 scale) and |c - off| at most 8: then float32 and float64 agree, and
+    # float32 takes a quarter of the memory traffic. An fp32 scale needs float64.
+    wide = np.float32 if act in ("bf16", "fp16") else np.float64
+    codes = codes.reshape(-1, group_size).astype(wide) - wide(1 << (num_bits - 1))
+    s = round_to(to_np(flat_scale).astype(np.float32), act).astype(wide)
     return round_to(codes * s.reshape(-1, 1), act).reshape(-1)
 
 
@@ -301,16 +305,27 @@ def silu_round(g, act):
         return round_to(g / (np.float32(1.0) + np.exp(-g)), act)
 
 
-def expert_stages(x, blob, act):
+def expert_stages(x, blob, act, weights=None):
     """One expert's stock stages for rows `x` [n, hidden] (float32 values of `act`):
     (h, y) with h = act(x Wg^T) * (x Wu^T) and y = h Wd^T, each rounded to `act`
-    (vaayu/packed_expert_kernels.py:408-409)."""
-    wg, wd, wu = expert_weights(blob, act)
+    (vaayu/packed_expert_kernels.py:408-409). `weights`: the expert's dequantized
+    (gate, down, up), when the caller already holds them."""
+    wg, wd, wu = weights if weights is not None else expert_weights(blob, act)
     g = _linear(x, wg, act)
     u = _linear(x, wu, act)
     h = round_to(silu_round(g, act).astype(np.float64) * u.astype(np.float64), act)
     y = _linear(h, wd, act)
     return h, y
+
+
+def truth_stages(x, exact_weights):
+    """The fp64 truth of one expert (tests/test_packed_prefill_kernels.py:100-116): the
+    checkpoint's exact weights (gate, down, up) as float64, no rounding anywhere.
+    Returns y = (silu(x Wg^T) * (x Wu^T)) Wd^T, float64."""
+    wg, wd, wu = (np.asarray(w, dtype=np.float64) for w in exact_weights)
+    xv = np.asarray(x, dtype=np.float64)
+    g, u = xv @ wg.T, xv @ wu.T
+    return (g / (1.0 + np.exp(-g)) * u) @ wd.T
 
 
 def contribution(y, w, w_dtype, act):
@@ -404,12 +419,14 @@ def prefill_stages(x, eidx, blobs, act="bf16"):
     return h, y
 
 
-def stock_prefill(x, eidx, routing_weights, blobs, w_dtype=None, act="bf16") -> np.ndarray:
+def stock_prefill(x, eidx, routing_weights, blobs, w_dtype=None, act="bf16",
+                  weights_of=None) -> np.ndarray:
     """`stock_experts_prefill(linear=_linear_fp32)` (vaayu/packed_expert_kernels.py:780-814),
     correctly rounded: per live expert in id order, its rows' rounded stages times their
     weights, added into each token's fp32 row in expert-id order (the order
     `accumulate_expert_outputs` sums in, vaayu/moe_patch.py:914-940). A routed expert
-    with no entry is skipped."""
+    with no entry is skipped. `weights_of(expert id)`: its dequantized (gate, down, up),
+    when the caller holds them (otherwise dequantized here)."""
     act = act_name(act)
     xv = to_np(x)
     e = np.asarray(to_np(eidx), dtype=np.int64)
@@ -425,7 +442,8 @@ def stock_prefill(x, eidx, routing_weights, blobs, w_dtype=None, act="bf16") -> 
         at += c
         if ex not in blobs:
             continue
-        _h, y = expert_stages(xv[rows // top_k], blobs[ex], act)
+        wts = weights_of(ex) if weights_of is not None else None
+        _h, y = expert_stages(xv[rows // top_k], blobs[ex], act, weights=wts)
         contrib = contribution(y, rw[rows][:, None], w_dtype, act)
         for i, r in enumerate(rows.tolist()):          # sequential: a token may repeat
             t = r // top_k

@@ -50,3 +50,36 @@ def test_odd_word_counts_and_tails():
         got = mp._hip_dequant(words, scale, 4, 8, torch.bfloat16)
         want = O.dequant_flat(words.cpu(), scale.cpu(), 4, 8, "bf16")
         assert np.array_equal(got.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 128), (8, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_per_role_dequant_equals_the_hip_blob_dequant(bits, gs, dtype):
+    """`dequantize_packed_weight` (eager torch on the GPU, one role at a time) and the
+    blob's one-launch HIP dequant give the same bits (tests/test_packed_expert_dequant.py:
+    368-381)."""
+    from vaayu_amd.moe_patch import (build_expert_blob, dequantize_expert_blob,
+                                     dequantize_packed_weight)
+    from vaayu_amd.synth import quantize_pack
+    g = torch.Generator().manual_seed(bits + gs)
+    by_role = {}
+    for role, shape in (("gate", (768, 2048)), ("down", (2048, 768)), ("up", (768, 2048))):
+        w = (torch.randn(shape, generator=g) * 0.02).bfloat16()
+        packed, scale = quantize_pack(w, bits, gs, torch.float16)
+        by_role[role] = {"weight_packed": packed.cuda(), "weight_scale": scale.cuda(),
+                         "weight_shape": torch.tensor(list(shape))}
+    via_hip = dequantize_expert_blob(build_expert_blob(by_role), dtype)
+    for role, comps in by_role.items():
+        assert torch.equal(dequantize_packed_weight(comps, dtype), via_hip[role]), role
+
+
+def test_a_stream_off_16_bytes_takes_the_eager_path():
+    """The kernel reads 16-byte units; a view starting one word in is dequantized by the
+    eager arithmetic, with the same bits."""
+    rng = np.random.default_rng(5)
+    words = torch.from_numpy(rng.integers(-2 ** 31, 2 ** 31, 257, dtype=np.int64)
+                             .astype(np.int32)).cuda()
+    scale = torch.from_numpy(rng.uniform(0.001, 0.1, 257).astype(np.float32)).half().cuda()
+    got = mp._hip_dequant(words[1:], scale[1:], 4, 8, torch.bfloat16)
+    want = O.dequant_flat(words[1:].cpu(), scale[1:].cpu(), 4, 8, "bf16")
+    assert np.array_equal(got.float().cpu().numpy(), want)

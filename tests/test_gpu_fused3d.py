@@ -128,3 +128,26 @@ def test_bad_calls_raise():
         mod.forward(x.bfloat16(), idx + 4, w.to(DEV))        # expert id out of range
     with pytest.raises(ValueError):
         mod.forward(x.bfloat16(), idx[:3], w[:3].to(DEV))    # shapes disagree
+
+
+def test_a_call_split_into_token_chunks_gives_the_same_bits(monkeypatch):
+    """With the kernels' offset limit lowered to 40 KiB the forward launches in token
+    chunks of 20; the result equals the one-launch call bit for bit."""
+    import vaayu_amd.packed_expert_kernels as pk
+    E, H, I, k, T = 8, 256, 128, 2, 200
+    layer = random_layer(E, H, I, seed=70)
+    mod = to_module(layer)
+    idx, w = routing(T, E, k, seed=71)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(72)).bfloat16().to(DEV)
+    whole = mod.forward(x, idx, w.to(DEV))
+    monkeypatch.setattr(pk, "_OFFSET_LIMIT", 40 << 10)
+    step = pk._tokens_per_launch(mod.Hp, mod.Ip, k, E)
+    assert step * 3 < T, "premise: the lowered limit splits the call"
+    parts = []
+    real = mod._forward_part
+    monkeypatch.setattr(mod, "_forward_part",
+                        lambda *a: (parts.append(a[0].shape[0]), real(*a)))
+    split = mod.forward(x, idx, w.to(DEV))
+    torch.cuda.synchronize()
+    assert len(parts) == -(-T // step) and sum(parts) == T
+    assert torch.equal(split, whole)

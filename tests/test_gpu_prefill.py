@@ -298,3 +298,43 @@ def test_fp16_activations():
                                              scale_dtype=torch.float16)
     got = _launch(x, eidx, w, blobs)
     assert rel(got, O.stock_prefill(x, eidx, w, cblobs, act="fp16")) <= 2e-3
+
+
+def test_a_call_split_into_token_chunks_gives_the_same_bits(monkeypatch):
+    """With the offset limit lowered to 512 KiB `_prefill_launch` runs the call in token
+    chunks (25 tokens each); each token's output equals the one-launch call's bit for bit (batch
+    invariance), and the chunks cover the call in order."""
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, tokens=300, top_k=6)
+    whole = _launch(x, eidx, w, blobs)
+    monkeypatch.setattr(pk, "_OFFSET_LIMIT", 512 << 10)
+    step = pk._tokens_per_launch(QWEN[0], QWEN[1], 6, len(set(eidx.reshape(-1).tolist())))
+    assert step * 3 < 300, "premise: the lowered limit splits the call"
+    parts = []
+    real = pk._prefill_call
+    monkeypatch.setattr(pk, "_prefill_call",
+                        lambda x_, e_, w_, b_, o_, p_: (parts.append(x_.shape[0]),
+                                                        real(x_, e_, w_, b_, o_, p_)))
+    split = _launch(x, eidx, w, blobs)
+    assert len(parts) == -(-300 // step) and sum(parts) == 300
+    assert torch.equal(split, whole)
+
+
+def test_the_library_refuses_a_launch_past_its_offset_range():
+    """A launch whose tables could hold rows past the 32-bit offset range returns an error
+    before anything is launched (the check reads only the sizes)."""
+    lib = pk._require_backend()
+    from vaayu_amd import _lib
+    blob = gpu_blobs(*QWEN, 1)[0]
+    g = _lib.geom_struct(blob["geom"])
+    buf = torch.zeros(64, dtype=torch.int64, device="cuda")
+    huge = (0xF0000000 // (2 * QWEN[1])) // 16 + 1                 # h rows one block past
+    rc = lib.vaayu_prefill_down(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
+                                2, buf.data_ptr(), huge, g, 0, 0, 0,
+                                _lib.stream_ptr(buf.device))
+    assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
+    tokens_over = (0xF0000000 // (2 * QWEN[0])) + 1                 # x rows one token past
+    rc = lib.vaayu_prefill_gate_up(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
+                                   buf.data_ptr(), -(-tokens_over // 16), 1, g, 0, 0,
+                                   _lib.stream_ptr(buf.device))
+    assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
+    torch.cuda.synchronize()

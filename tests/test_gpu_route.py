@@ -78,6 +78,28 @@ def test_rejections_raise():
         route_topk(torch.randn(1, 32, device=DEV), 4, top_p=0.0)
 
 
+def test_output_buffers_are_checked_before_the_launch():
+    """Caller-given weights / ids must be contiguous fp32 / int64 [tokens, n] on the logits'
+    device: the kernel writes through their pointers. Logits of another dtype are refused."""
+    logits = torch.randn(3, 32, device=DEV)
+    bad = [dict(weights=torch.empty(3, 2, device=DEV)),                       # too small
+           dict(weights=torch.empty(3, 4, device=DEV, dtype=torch.bfloat16)),
+           dict(weights=torch.empty(4, 3, device=DEV).t()),                   # not contiguous
+           dict(ids=torch.empty(3, 4, device=DEV, dtype=torch.int32)),
+           dict(ids=torch.empty(3, 4, dtype=torch.int64))]                    # host memory
+    for kw in bad:
+        with pytest.raises(ValueError):
+            route_topk(logits, 4, **kw)
+    with pytest.raises(ValueError):
+        route_topk(logits.double(), 4)
+    w, ids = torch.empty(3, 4, device=DEV), torch.empty(3, 4, device=DEV, dtype=torch.int64)
+    got_w, got_ids = route_topk(logits, 4, weights=w, ids=ids)
+    torch.cuda.synchronize()
+    assert got_w.data_ptr() == w.data_ptr() and got_ids.data_ptr() == ids.data_ptr()
+    want_w, want_ids = route_topk(logits, 4)
+    assert torch.equal(w, want_w) and torch.equal(ids, want_ids)
+
+
 @pytest.mark.parametrize("experts,top_k,keep_k,top_p", [
     (128, 8, 6, None), (128, 8, None, 0.7), (256, 8, 5, 0.6), (64, 6, 6, 0.5),
     (512, 10, 4, None), (128, 8, None, 0.01), (128, 8, 1, None), (32, 4, 8, 0.95)])

@@ -3,8 +3,9 @@
 //   out[i] = round_out((code_i - 2^(bits-1)) * round_out(scale[i / group]))
 // The code offset is subtracted exactly in integers and the product is formed in fp32
 // (exact for bf16 / fp16 outputs; the fp32 output's own rounding for fp32), then rounded
-// once to the output dtype. Each thread handles one 16-byte unit (4 words) and writes its
-// 128/bits outputs with wide stores: a pure HBM stream.
+// once to the output dtype. Each thread takes one 16-byte unit (4 words): one 16-byte code
+// load, one scale load per word (a group holds whole words), and its 4 * 32/bits outputs
+// leave as 16-byte stores. HBM-bound: per word 4 code bytes in, 32/bits outputs out.
 #include "common.hpp"
 #include "abi_internal.hpp"
 
@@ -16,34 +17,58 @@ __device__ __forceinline__ float load_sc(const void* p, int64_t i, int dt) {
   return load_as_float<DT_FP32>(p, i);
 }
 
+// Output element type of dtype code OUT.
+template <int OUT> struct OutT { typedef uint16_t type; };
+template <> struct OutT<DT_FP32> { typedef float type; };
+
+template <int OUT>
+__device__ __forceinline__ typename OutT<OUT>::type out_bits(float v) {
+  if constexpr (OUT == DT_BF16) return __builtin_bit_cast(uint16_t, (__bf16)v);
+  else if constexpr (OUT == DT_FP16) return __builtin_bit_cast(uint16_t, (_Float16)v);
+  else return v;
+}
+
 template <int BITS, int OUT>
 __global__ void __launch_bounds__(256)
 dequant_kernel(const int32_t* __restrict__ packed, const void* __restrict__ scale, int sc_dt,
                void* __restrict__ out, int64_t n_words, int group) {
-  constexpr int PER = 32 / BITS;
+  constexpr int PER = 32 / BITS;                        // codes per word
   constexpr uint32_t mask = (1u << BITS) - 1u;
+  typedef typename OutT<OUT>::type T;
+  constexpr int PER_VEC = 16 / sizeof(T);               // outputs per 16-byte store
   const int64_t w0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (w0 >= n_words) return;
-  uint32_t w[4];
   const int nw = n_words - w0 >= 4 ? 4 : (int)(n_words - w0);
-  if (nw == 4 && ((uintptr_t)(packed + w0) & 15) == 0) {
-    const uint4 v = *(const uint4*)(packed + w0);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  float s[4];
+  if (nw == 4) {
+    const uint4 v = *(const uint4*)(packed + w0);       // w0 * 4 bytes: 16-byte aligned
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
   } else {
-    for (int i = 0; i < 4; ++i) w[i] = i < nw ? (uint32_t)packed[w0 + i] : 0u;
+    for (int i = 0; i < nw; ++i) w[i] = (uint32_t)packed[w0 + i];
   }
-  for (int i = 0; i < nw; ++i) {
-    const int64_t e0 = (w0 + i) * PER;
-    float vals[PER];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    s[i] = round_act<OUT>(load_sc(scale, (i < nw ? w0 + i : w0) * PER / group, sc_dt));
+  T vals[4 * PER];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int64_t e = e0 + j;
-      const float s = round_act<OUT>(load_sc(scale, e / group, sc_dt));
       const int c = (int)((w[i] >> (j * BITS)) & mask) - (1 << (BITS - 1));
-      vals[j] = round_act<OUT>((float)c * s);
+      vals[i * PER + j] = out_bits<OUT>((float)c * s[i]);
     }
+  T* dst = (T*)out + w0 * PER;
+  if (nw == 4) {                                        // 4 * PER * sizeof(T) is a multiple of 16
 #pragma unroll
-    for (int j = 0; j < PER; ++j) store_act<OUT>(out, e0 + j, vals[j]);
+    for (int v = 0; v < 4 * PER / PER_VEC; ++v)
+    {
+      uint4 chunk;
+      __builtin_memcpy(&chunk, vals + v * PER_VEC, 16);
+      *(uint4*)(dst + v * PER_VEC) = chunk;
+    }
+  } else {
+    for (int e = 0; e < nw * PER; ++e) dst[e] = vals[e];
   }
 }
 
@@ -61,6 +86,8 @@ extern "C" int vaayu_dequant_blob(const int32_t* packed, const void* scale, int3
   if (group <= 0 || group % (32 / bits)) return set_error(-2, "group size");
   if (scale_dtype < 0 || scale_dtype > 2 || out_dtype < 0 || out_dtype > 2)
     return set_error(-1, "dtype code");
+  if (((uintptr_t)packed & 15) || ((uintptr_t)out & 15))
+    return set_error(-2, "codes and output must start on 16 bytes");
   const int64_t units = (n_words + 3) / 4;
   const dim3 grid((unsigned)((units + 255) / 256)), block(256);
   hipStream_t st = (hipStream_t)stream;

@@ -194,6 +194,8 @@ extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const i
     return set_error(-1, "null pointer argument");
   if (int rc = fused3d_check(n_blocks, top_k, hidden, hidden_pad, inter)) return rc;
   if (inter_pad < inter) return set_error(-2, "h's row pitch is below the intermediate size");
+  if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * hidden_pad, 0))
+    return set_error(-2, why);
   if (n_blocks == 0) return 0;
   Fused3DArgs p;
   p.rows = rows; p.tbl = tbl; p.btbl = btbl;
@@ -215,6 +217,8 @@ extern "C" int vaayu_fused3d_down(const void* h, const int64_t* rows, const int6
   if (!h || !rows || !tbl || !btbl || !gammas || !y || !codes_end || !scales_end)
     return set_error(-1, "null pointer argument");
   if (int rc = fused3d_check(n_blocks, top_k, inter, inter_pad, hidden)) return rc;
+  if (const char* why = rows_out_of_reach(n_blocks, 1, 0, 2ll * inter_pad))
+    return set_error(-2, why);
   if (n_blocks == 0) return 0;
   Fused3DArgs p;
   p.rows = rows; p.tbl = tbl; p.btbl = btbl;

@@ -60,6 +60,8 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
   if (n_blocks <= 0 || top_k <= 0) return set_error(-1, "n_blocks / top_k must be positive");
   if (scale_dtype < 0 || scale_dtype > 3) return set_error(-1, "scale dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
+  if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * g->hidden, 0))
+    return set_error(-2, why);
   const PrefillArgs p{n_blocks, (g->inter + kTileN - 1) / kTileN, top_k, g->hidden, g->inter,
                       log2_of(g->group),
                       g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype};
@@ -90,6 +92,8 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
   if (scale_dtype < 0 || scale_dtype > 3 || rw_dtype < 0 || rw_dtype > 2)
     return set_error(-1, "scale / routing-weight dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
+  if (const char* why = rows_out_of_reach(n_blocks, 1, 0, 2ll * g->inter))
+    return set_error(-2, why);
   const PrefillArgs p{n_blocks, (g->hidden + kTileN - 1) / kTileN, 1, g->hidden, g->inter,
                       log2_of(g->group),
                       g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype};

@@ -114,6 +114,25 @@ __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
 // K offset added to it.
 constexpr uint32_t kNoRow = 0xFFFF0000u;
 
+// Activation rows (x, one per token) and intermediate rows (h, one per table row) are
+// addressed with 32-bit byte offsets. A launch's tables hold at most n_blocks * 16 row ids
+// (token * top_k + slot), so a launch whose rows could start past kOffsetLimit bytes is
+// refused: callers split such a call into token chunks. The limit leaves room below kNoRow
+// for any K offset inside a row.
+constexpr int64_t kOffsetLimit = 0xF0000000ll;
+
+// Why a launch over n_blocks table blocks could address past the limit, or nullptr:
+// x_row_bytes for rows read per token (gate/up), h_row_bytes per table row (down).
+inline const char* rows_out_of_reach(int n_blocks, int top_k, int64_t x_row_bytes,
+                                     int64_t h_row_bytes) {
+  const int64_t rows = (int64_t)n_blocks * 16;
+  if ((rows + top_k - 1) / top_k * x_row_bytes > kOffsetLimit)
+    return "activation rows past the 32-bit offset range: launch fewer tokens per call";
+  if (rows * h_row_bytes > kOffsetLimit)
+    return "intermediate rows past the 32-bit offset range: launch fewer tokens per call";
+  return nullptr;
+}
+
 // One K step of a run's activation rows (S*16 rows x KS codes, RB = KS*2 bytes a row) lives
 // in LDS as S*16 rows of RB bytes, row r's 16-byte piece c at position c ^ (r % PPR): the
 // A reads of one MFMA (16 rows at one piece) then fall on distinct banks. Rows reach LDS by

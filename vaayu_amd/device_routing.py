@@ -55,6 +55,8 @@ def route_topk(logits, top_k: int, renorm: bool = True, keep_k=None, top_p=None,
     fp32 [..., n], ids int64 [..., n]), n = min(keep_k, top_k). Equal probabilities go to
     the lower expert id. `weights` / `ids` given (contiguous [tokens, n]): written in place."""
     lib = pk._require_backend()
+    if logits.dtype not in pk._DTYPE_CODE:
+        raise ValueError(f"logits must be bf16, fp16 or fp32, got {logits.dtype}")
     n_out, keep, p = _budget(top_k, keep_k, top_p)
     experts = logits.shape[-1]
     lead = logits.shape[:-1]
@@ -66,6 +68,12 @@ def route_topk(logits, top_k: int, renorm: bool = True, keep_k=None, top_p=None,
         weights = torch.empty(tokens, n_out, dtype=torch.float32, device=logits.device)
     if ids is None:
         ids = torch.empty(tokens, n_out, dtype=torch.int64, device=logits.device)
+    for what, t, dt in (("weights", weights, torch.float32), ("ids", ids, torch.int64)):
+        # the kernel writes tokens x n_out entries through the raw pointer
+        if (t.dtype != dt or not t.is_contiguous() or t.device != logits.device
+                or t.numel() != tokens * n_out):
+            raise ValueError(f"{what} must be a contiguous {dt} tensor of {tokens} x {n_out} "
+                             f"on {logits.device}, got {t.dtype} {tuple(t.shape)} on {t.device}")
     rc = lib.vaayu_route_topk(flat.data_ptr(), pk._DTYPE_CODE[flat.dtype], tokens, experts,
                               top_k, keep, p, int(renorm), weights.data_ptr(), ids.data_ptr(),
                               None, None, _lib.stream_ptr(logits.device))

@@ -126,6 +126,16 @@ class Fused3DExperts:
         out = torch.empty(T, self.H, dtype=torch.float32, device=x.device)
         if T == 0:
             return out.to(x.dtype)
+        # the kernels address x and h rows with 32-bit offsets: a larger call runs in token
+        # chunks, with the same bits (a row's arithmetic does not depend on its launch-mates)
+        step = pk._tokens_per_launch(self.Hp, self.Ip, top_k, self.E)
+        for t0 in range(0, T, step):
+            part = slice(t0, min(t0 + step, T))
+            self._forward_part(x[part], expert_ids[part], routing_weights[part], out[part])
+        return out.to(x.dtype)
+
+    def _forward_part(self, x, expert_ids, routing_weights, out) -> None:
+        T, top_k = expert_ids.shape
         gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks = self.tables(expert_ids)
         if self.Hp == self.H and x.is_contiguous():
             xp = x
@@ -138,7 +148,6 @@ class Fused3DExperts:
         gammas = routing_weights.reshape(-1).to(torch.float32).contiguous()
         self.launch(xp, h, y, out, (gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks), gammas,
                     top_k)
-        return out.to(x.dtype)
 
     def launch(self, xp, h, y, out, tables, gammas, top_k) -> None:
         """The three kernels on prepared buffers (what `forward` runs; allocates nothing, so

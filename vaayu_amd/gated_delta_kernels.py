@@ -13,12 +13,13 @@ launches per mixer per token. Each seam here is one hand-written HIP kernel
   conv  one thread per (batch, channel): shift, append, depthwise dot, silu, in place.
   norm  one wave per row.
 
-Detection, the self-checks and the installer behave as the reference's (file:line cited per
-function): a seam is found by the surface it needs, never by class or architecture name;
-each fused seam is checked against the stock one on the device before it goes in, and one
-that disagrees stays stock with a WARNING. Without the built library `triton` is None and
-nothing is installed (the reference's "no Triton" state); a direct kernel call then raises
-ImportError.
+The host side is a table of seam descriptors (`_Seam`): how a mixer exposes the seam (by
+its surface, never by class or architecture name), what callable is there now, the key
+its verdict is kept under, the on-device self-check against the stock seam, and how the
+fused seam is put in. A seam whose check disagrees stays stock with a WARNING; a fused
+seam carries the stock callable it replaced under `_MARK`, so installing twice is a
+no-op. Without the built library `triton` is None and nothing is installed (the
+reference's "no Triton" state); a direct kernel call then raises ImportError.
 """
 import ctypes
 import math
@@ -30,27 +31,25 @@ from . import _lib
 
 try:
     _lib.load()
-    _BACKEND = _lib
+    _BACKEND, _LOAD_ERROR = _lib, None
 except ImportError as _exc:              # reported at the first kernel call
-    _BACKEND = None
-    _LOAD_ERROR = str(_exc)
+    _BACKEND, _LOAD_ERROR = None, str(_exc)
 
-# Truthiness of the kernel backend, under the name the reference's installer and tests use
-# for it (they set it to None to simulate a machine without the kernels).
+# The kernel backend's truthiness under the name the reference's installer and tests use
+# (they set it to None to stand for a machine without the kernels).
 triton = _BACKEND
 
-# Every fused seam carries the stock callable it replaced under this attribute
+# A fused seam carries the stock callable it replaced under this attribute
 # (vaayu/gated_delta_kernels.py:31-33).
 _MARK = "_vaayu_fused"
 # Self-check tolerance on seam outputs, relative L2 against the stock seam (:34-37).
 _CHECK_TOL = 5e-2
-_ATTR = {"rule": "recurrent_gated_delta_rule", "conv": "causal_conv1d_update"}
 _DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
 def _require_backend():
     if triton is None:
-        raise ImportError(globals().get("_LOAD_ERROR", "vaayu_amd kernels unavailable"))
+        raise ImportError(_LOAD_ERROR or "vaayu_amd kernels unavailable")
     return _lib.load()
 
 
@@ -66,25 +65,7 @@ def _code(t, what):
         raise TypeError(f"{what} must be bf16, fp16 or fp32, got {t.dtype}") from None
 
 
-def gated_delta_seams(model) -> dict:
-    """{"rule": [...], "conv": [...], "norm": [...]}: every gated-delta mixer under `model`
-    (itself included) exposing each seam (vaayu/gated_delta_kernels.py:43-61). A mixer is a
-    module with a callable `recurrent_gated_delta_rule`; its `norm` counts only with a 1-D
-    `weight` and a float `variance_epsilon` (the gated RMSNorm's surface)."""
-    seams = {"rule": [], "conv": [], "norm": []}
-    for module in model.modules():
-        if not callable(getattr(module, "recurrent_gated_delta_rule", None)):
-            continue
-        seams["rule"].append(module)
-        if callable(getattr(module, "causal_conv1d_update", None)):
-            seams["conv"].append(module)
-        norm = getattr(module, "norm", None)
-        weight = getattr(norm, "weight", None)
-        if (isinstance(weight, torch.Tensor) and weight.dim() == 1
-                and isinstance(getattr(norm, "variance_epsilon", None), float)):
-            seams["norm"].append(module)
-    return seams
-
+# ── the three kernels ────────────────────────────────────────────────────────────────────
 
 def fused_recurrent_rule(query, key, value, g, beta, initial_state, output_final_state,
                          use_qk_l2norm_in_kernel=False):
@@ -157,9 +138,17 @@ def fused_gated_norm(weight, eps, hidden_states, gate):
     return o.view(hidden_states.shape)
 
 
+# ── fused seams ──────────────────────────────────────────────────────────────────────────
+
+def _marked(fn, stock):
+    setattr(fn, _MARK, stock)
+    return fn
+
+
 def _patch_norm(norm):
-    """Patch the norm's forward IN PLACE, reading `norm.weight` at call time: a streamed
-    layer's Parameters are replaced on every load (vaayu/gated_delta_kernels.py:238-249)."""
+    """Replace the norm's forward IN PLACE with one that reads `norm.weight` at call time
+    (a streamed layer's Parameters are replaced on every load; vaayu/gated_delta_kernels.py:
+    238-249). A call without a gate goes to the stock forward."""
     stock = norm.forward
 
     def forward(hidden_states, gate=None):
@@ -167,8 +156,7 @@ def _patch_norm(norm):
             return stock(hidden_states, gate)
         return fused_gated_norm(norm.weight, norm.variance_epsilon, hidden_states, gate)
 
-    setattr(forward, _MARK, stock)
-    norm.forward = forward
+    norm.forward = _marked(forward, stock)
 
 
 def _rule_seam(stock):
@@ -176,104 +164,168 @@ def _rule_seam(stock):
              use_qk_l2norm_in_kernel=False):
         return fused_recurrent_rule(query, key, value, g, beta, initial_state,
                                     output_final_state, use_qk_l2norm_in_kernel)
-
-    setattr(seam, _MARK, stock)
-    return seam
+    return _marked(seam, stock)
 
 
 def _conv_seam(stock):
-    """Multi-token calls go to the stock seam; HF's decode path never sends them
+    """Multi-token calls go to the stock seam; transformers' decode path never sends them
     (vaayu/gated_delta_kernels.py:193-200)."""
     def seam(hidden_states, conv_state, weight, bias=None, activation=None):
         if hidden_states.shape[-1] != 1:
             return stock(hidden_states, conv_state, weight, bias, activation)
         return fused_conv_update(hidden_states, conv_state, weight, bias, activation)
+    return _marked(seam, stock)
 
-    setattr(seam, _MARK, stock)
-    return seam
 
+# ── self-checks: stock against fused on the device, at the mixer's decode geometry ──────
 
 def _rel(a, b) -> float:
     a, b = a.float(), b.float()
     return ((a - b).norm() / b.norm().clamp_min(1e-12)).item()
 
 
-def _randn(gen, device, *shape):
-    return torch.randn(*shape, generator=gen, device=device)
-
-
 def _rule_geometry(mixer):
-    """(HV, K, V) read off the mixer when it exposes them, else a tiny fallback
-    (vaayu/gated_delta_kernels.py:275-280): the self-check runs the geometry decode uses."""
-    hv, k, v = (getattr(mixer, "num_v_heads", None), getattr(mixer, "head_k_dim", None),
-                getattr(mixer, "head_v_dim", None))
-    if isinstance(hv, int) and isinstance(k, int) and isinstance(v, int):
-        return hv, k, v
-    return 2, 16, 16
+    """(HV, K, V) as the mixer declares them, else a tiny stand-in (vaayu/gated_delta_kernels.
+    py:275-280): the check should run the geometry decode will."""
+    dims = tuple(getattr(mixer, a, None) for a in ("num_v_heads", "head_k_dim", "head_v_dim"))
+    return dims if all(isinstance(d, int) for d in dims) else (2, 16, 16)
 
 
 def _conv_geometry(mixer):
-    """(D, W) from the mixer's conv1d weight [D, 1, W], shape only (:283-288)."""
+    """(D, W) from the mixer's conv1d weight [D, 1, W], by shape only (safe on the meta
+    device; :283-288), else a stand-in."""
     weight = getattr(getattr(mixer, "conv1d", None), "weight", None)
     if isinstance(weight, torch.Tensor) and weight.dim() == 3:
-        d, _, w = weight.shape
-        return d, w
+        return weight.shape[0], weight.shape[2]
     return 64, 4
 
 
+class _Draw:
+    """Seeded random tensors on one device, made in the dtype asked for."""
+
+    def __init__(self, device):
+        self.device = device
+        self.gen = torch.Generator(device=device).manual_seed(0)
+
+    def normal(self, *shape, dtype=torch.float32, scale=1.0):
+        return (torch.randn(*shape, generator=self.gen, device=self.device) * scale).to(dtype)
+
+    def uniform(self, *shape, dtype=torch.float32):
+        return torch.rand(*shape, generator=self.gen, device=self.device).to(dtype)
+
+
 def _check_rule(stock, device, dtype, geom) -> float:
-    """Stock vs fused at B=1, T=1 on random inputs in the model's dtype (:295-307)."""
-    HV, K, V = geom
-    gen = torch.Generator(device=device).manual_seed(0)
-    q = _randn(gen, device, 1, 1, HV, K).to(dtype)
-    k = _randn(gen, device, 1, 1, HV, K).to(dtype)
-    v = _randn(gen, device, 1, 1, HV, V).to(dtype)
-    g = -torch.rand(1, 1, HV, generator=gen, device=device)
-    beta = torch.rand(1, 1, HV, generator=gen, device=device).to(dtype)
-    h0 = (_randn(gen, device, 1, HV, K, V) * 0.1).to(dtype)
-    kw = dict(g=g, beta=beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
-    so, sh = stock(q, k, v, initial_state=h0.clone(), **kw)
-    fo, fh = fused_recurrent_rule(q, k, v, initial_state=h0.clone(), **kw)
-    return max(_rel(fo, so), _rel(fh, sh))
+    """relL2 of the fused rule against `stock` at one decode step (B = T = 1, l2 norm on),
+    output and final state, on random inputs in the model's dtype (:295-307)."""
+    heads, k_dim, v_dim = geom
+    d = _Draw(device)
+    q, k = d.normal(1, 1, heads, k_dim, dtype=dtype), d.normal(1, 1, heads, k_dim, dtype=dtype)
+    v = d.normal(1, 1, heads, v_dim, dtype=dtype)
+    args = dict(g=-d.uniform(1, 1, heads), beta=d.uniform(1, 1, heads, dtype=dtype),
+                output_final_state=True, use_qk_l2norm_in_kernel=True)
+    state = d.normal(1, heads, k_dim, v_dim, dtype=dtype, scale=0.1)
+    want_o, want_h = stock(q, k, v, initial_state=state.clone(), **args)
+    got_o, got_h = fused_recurrent_rule(q, k, v, initial_state=state.clone(), **args)
+    return max(_rel(got_o, want_o), _rel(got_h, want_h))
 
 
 def _check_conv(stock, device, dtype, geom) -> float:
-    """inf unless the conv state is bit-identical to the stock seam's (:310-320)."""
-    D, W = geom
-    gen = torch.Generator(device=device).manual_seed(0)
-    x = _randn(gen, device, 1, 1, D).to(dtype).transpose(1, 2)
-    state = _randn(gen, device, 1, W, D).to(dtype).transpose(1, 2)
-    w = _randn(gen, device, D, W).to(dtype)
-    s_state, f_state = state.clone(), state.clone()
-    so = stock(x, s_state, w, None, "silu")
-    fo = fused_conv_update(x, f_state, w, None, "silu")
-    return _rel(fo, so) if torch.equal(f_state, s_state) else math.inf
+    """relL2 of the fused conv update's output, or inf unless the in-place state update is
+    bit-identical to the stock seam's (:310-320). Inputs as transformers passes them:
+    x [B, D, 1] and a channels-last state."""
+    channels, width = geom
+    d = _Draw(device)
+    x = d.normal(1, 1, channels, dtype=dtype).transpose(1, 2)
+    state = d.normal(1, width, channels, dtype=dtype).transpose(1, 2)
+    w = d.normal(channels, width, dtype=dtype)
+    stock_state, fused_state = state.clone(), state.clone()
+    want = stock(x, stock_state, w, None, "silu")
+    got = fused_conv_update(x, fused_state, w, None, "silu")
+    return _rel(got, want) if torch.equal(fused_state, stock_state) else math.inf
 
 
 def _check_norm(norm, device, dtype) -> float:
-    """A stand-in carries the weight: a streamed layer's own may be on the meta device
-    (:323-333). It also carries the norm's `activation` name, which newer transformers'
-    forward reads (a gate other than silu then fails the check and stays stock)."""
-    gen = torch.Generator(device=device).manual_seed(0)
+    """relL2 of the fused gated norm against the norm class's own forward, run on a
+    stand-in that carries a fresh weight (a streamed layer's may be on the meta device;
+    :323-333) and the norm's `activation` name (newer transformers reads it: a gate other
+    than silu then fails the check)."""
+    d = _Draw(device)
     n = norm.weight.numel()
-    stand_in = types.SimpleNamespace(weight=_randn(gen, device, n).to(norm.weight.dtype),
+    stand_in = types.SimpleNamespace(weight=d.normal(n, dtype=norm.weight.dtype),
                                      variance_epsilon=norm.variance_epsilon,
                                      activation=getattr(norm, "activation", "silu"))
-    x, z = (_randn(gen, device, 4, n).to(dtype) for _ in range(2))
-    so = type(norm).forward(stand_in, x, z)
-    fo = fused_gated_norm(stand_in.weight, stand_in.variance_epsilon, x, z)
-    return _rel(fo, so)
+    x, z = d.normal(4, n, dtype=dtype), d.normal(4, n, dtype=dtype)
+    want = type(norm).forward(stand_in, x, z)
+    return _rel(fused_gated_norm(stand_in.weight, stand_in.variance_epsilon, x, z), want)
 
 
-def _passes_self_check(seam, stock, mixer, device, dtype) -> bool:
-    """(vaayu/gated_delta_kernels.py:336-354)"""
+# ── the seam table ───────────────────────────────────────────────────────────────────────
+
+class _Seam:
+    """One kind of seam: `present(mixer)` (by surface), `current(mixer)` (the callable in
+    place now), `key(mixer, current)` (what its verdict depends on), `error(...)` (the
+    self-check's relL2, inf for a state mismatch) and `install(mixer, stock)`."""
+
+    def __init__(self, name, present, current, key, error, install):
+        self.name, self.present, self.current = name, present, current
+        self.key, self.error, self.install = key, error, install
+
+
+def _has_gated_norm(mixer) -> bool:
+    norm = getattr(mixer, "norm", None)
+    weight = getattr(norm, "weight", None)
+    return (isinstance(weight, torch.Tensor) and weight.dim() == 1
+            and isinstance(getattr(norm, "variance_epsilon", None), float))
+
+
+def _set_attr(attr, wrap):
+    def install(mixer, stock):
+        setattr(mixer, attr, wrap(stock))
+    return install
+
+
+# Looked up by name at call time, so the module's checks can be swapped (tests do).
+_SEAMS = (
+    _Seam("rule",
+          present=lambda m: True,
+          current=lambda m: m.recurrent_gated_delta_rule,
+          key=lambda m, cur: ("rule", cur, *_rule_geometry(m)),
+          error=lambda m, cur, dev, dt: _check_rule(cur, dev, dt, _rule_geometry(m)),
+          install=_set_attr("recurrent_gated_delta_rule", _rule_seam)),
+    _Seam("conv",
+          present=lambda m: callable(getattr(m, "causal_conv1d_update", None)),
+          current=lambda m: m.causal_conv1d_update,
+          key=lambda m, cur: ("conv", cur, *_conv_geometry(m)),
+          error=lambda m, cur, dev, dt: _check_conv(cur, dev, dt, _conv_geometry(m)),
+          install=_set_attr("causal_conv1d_update", _conv_seam)),
+    _Seam("norm",
+          present=_has_gated_norm,
+          current=lambda m: m.norm.forward,
+          key=lambda m, cur: ("norm", type(m.norm), m.norm.weight.numel(),
+                              m.norm.weight.dtype, m.norm.variance_epsilon),
+          error=lambda m, cur, dev, dt: _check_norm(m.norm, dev, dt),
+          install=lambda m, stock: _patch_norm(m.norm)),
+)
+
+
+def _is_mixer(module) -> bool:
+    return callable(getattr(module, "recurrent_gated_delta_rule", None))
+
+
+def gated_delta_seams(model) -> dict:
+    """{"rule": [...], "conv": [...], "norm": [...]}: every gated-delta mixer under `model`
+    (itself included) exposing each seam (vaayu/gated_delta_kernels.py:43-61). A mixer is a
+    module with a callable `recurrent_gated_delta_rule`; its `norm` counts only with a 1-D
+    `weight` and a float `variance_epsilon` (the gated RMSNorm's surface)."""
+    mixers = [m for m in model.modules() if _is_mixer(m)]
+    return {s.name: [m for m in mixers if s.present(m)] for s in _SEAMS}
+
+
+def _self_check(seam, mixer, stock, device, dtype) -> bool:
+    """True if the fused seam agrees with `stock` on the device; else one WARNING
+    (vaayu/gated_delta_kernels.py:336-354)."""
     try:
-        if seam == "norm":
-            err = _check_norm(mixer.norm, device, dtype)
-        elif seam == "rule":
-            err = _check_rule(stock, device, dtype, _rule_geometry(mixer))
-        else:
-            err = _check_conv(stock, device, dtype, _conv_geometry(mixer))
+        err = seam.error(mixer, stock, device, dtype)
     except Exception as exc:  # a launch failure, or a stock seam with another contract
         why = f"{type(exc).__name__}: {exc}"
     else:
@@ -281,18 +333,9 @@ def _passes_self_check(seam, stock, mixer, device, dtype) -> bool:
             return True
         why = ("its conv state is not bit-identical to the stock seam's" if math.isinf(err)
                else f"relL2 {err:.2e} vs the stock seam, tolerance {_CHECK_TOL:.0e}")
-    print(f"[Vaayu] WARNING: fused gated-delta '{seam}' kernel failed its self-check "
+    print(f"[Vaayu] WARNING: fused gated-delta '{seam.name}' kernel failed its self-check "
           f"({why}); that seam stays on the stock torch path")
     return False
-
-
-def _install(seam, mixer, stock):
-    if seam == "norm":
-        _patch_norm(mixer.norm)
-    elif seam == "rule":
-        mixer.recurrent_gated_delta_rule = _rule_seam(stock)
-    else:
-        mixer.causal_conv1d_update = _conv_seam(stock)
 
 
 def install_gated_delta_kernels(hf_model, device, dtype) -> dict:
@@ -302,31 +345,26 @@ def install_gated_delta_kernels(hf_model, device, dtype) -> dict:
     installed off the GPU or without the kernel library, nor -- all-zero counts, nothing
     touched -- when `device` names a GPU index that is not the current one (the kernels
     launch on the current device's stream)."""
-    counts = {"rule": 0, "conv": 0, "norm": 0}
-    if triton is None or torch.device(device).type != "cuda":
+    counts = {s.name: 0 for s in _SEAMS}
+    dev = torch.device(device)
+    if triton is None or dev.type != "cuda":
         return counts
-    dev_index = torch.device(device).index
-    if dev_index is not None and dev_index != torch.cuda.current_device():
+    if dev.index is not None and dev.index != torch.cuda.current_device():
         print(f"[Vaayu] WARNING: fused gated-delta kernels not installed: model device {device} "
               f"is not the current CUDA device ({torch.cuda.current_device()}); decode keeps the "
               f"stock torch path")
         return counts
-    verdicts = {}
-    for seam, mixers in gated_delta_seams(hf_model).items():
-        for mixer in mixers:
-            current = mixer.norm.forward if seam == "norm" else getattr(mixer, _ATTR[seam])
-            if not hasattr(current, _MARK):
-                if seam == "norm":
-                    key = (seam, type(mixer.norm), mixer.norm.weight.numel(),
-                           mixer.norm.weight.dtype, mixer.norm.variance_epsilon)
-                elif seam == "rule":
-                    key = (seam, current, *_rule_geometry(mixer))
-                else:
-                    key = (seam, current, *_conv_geometry(mixer))
+    verdicts = {}            # one self-check per (seam, stock callable / class, geometry)
+    found = gated_delta_seams(hf_model)
+    for seam in _SEAMS:
+        for mixer in found[seam.name]:
+            stock = seam.current(mixer)
+            if not hasattr(stock, _MARK):
+                key = seam.key(mixer, stock)
                 if key not in verdicts:
-                    verdicts[key] = _passes_self_check(seam, current, mixer, device, dtype)
+                    verdicts[key] = _self_check(seam, mixer, stock, device, dtype)
                 if not verdicts[key]:
                     continue
-                _install(seam, mixer, current)
-            counts[seam] += 1
+                seam.install(mixer, stock)
+            counts[seam.name] += 1
     return counts

@@ -131,12 +131,15 @@ def _fused_dequant_kernel(flat_packed, flat_scale, num_bits, group_size, dtype):
 
 
 def _hip_dequant(flat_packed, flat_scale, num_bits, group_size, dtype):
-    """`_fused_dequant_kernel` on the GPU: one HIP launch, the same bits."""
+    """`_fused_dequant_kernel` on the GPU: one HIP launch, the same bits. The kernel reads
+    codes in 16-byte units; a stream that does not start on 16 bytes takes the eager path."""
+    packed = flat_packed.contiguous()
+    scale = flat_scale.contiguous()
+    if packed.data_ptr() % 16:
+        return _fused_dequant_kernel(packed, scale, num_bits, group_size, dtype)
     lib = _lib.load()
     out = torch.empty(flat_packed.numel() * (32 // num_bits), dtype=dtype,
                       device=flat_packed.device)
-    packed = flat_packed.contiguous()
-    scale = flat_scale.contiguous()
     rc = lib.vaayu_dequant_blob(packed.data_ptr(), scale.data_ptr(),
                                 _lib.DTYPE_CODE[scale.dtype], out.data_ptr(),
                                 _lib.DTYPE_CODE[dtype], packed.numel(), num_bits, group_size,

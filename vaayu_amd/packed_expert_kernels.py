@@ -1,163 +1,228 @@
 """Packed-expert routed-MoE kernels for MI355X: the drop-in for Vaayu's
 `vaayu/packed_expert_kernels.py`.
 
-The public entries, their arguments and results, the pointer tables, the verdict and
-fallback rules, the per-layer decode graph and the installer behave as the reference's
-(file:line cited per function), so the engine's fused forward (vaayu/moe_patch.py:2394-2401,
-2608-2624) and installer call (vaayu/vaayu_base.py:3560) need no change. The arithmetic
-runs in hand-written HIP kernels for gfx950 (vaayu_amd/csrc, C ABI in include/vaayu_amd.h):
+The engine's fused forward (vaayu/moe_patch.py:2394-2401, 2608-2624) and its installer call
+(vaayu/vaayu_base.py:3560) reach this module through the reference's names, arguments,
+results, table formats and WARNING lines; the arithmetic runs in hand-written gfx950 HIP
+kernels behind a C ABI (vaayu_amd/csrc, include/vaayu_amd.h):
 
-  decode  (one token)  `vaayu_decode_gate_up` + `vaayu_decode_down`: GEMVs on the VALU,
-                       codes unpacked in registers, the fp32 sum over pairs in table order.
+  decode  (one token)  `vaayu_decode_gate_up` + `vaayu_decode_down`: GEMVs over (blob, slot)
+                       pairs, codes dequantized in registers, the fp32 sum over pairs in
+                       table order.
   prefill (a call of   `vaayu_prefill_gate_up` + `vaayu_prefill_down` + `vaayu_prefill_reduce`:
-   any length)         grouped GEMMs on MFMA over 16-row blocks of one expert each, then
-                       each token's contributions summed in ascending expert id.
+   any length)         grouped GEMMs on MFMA over 16-row blocks of one expert each, then each
+                       token's contributions summed in ascending expert id.
+
+How the host side is organised here:
+
+  * `_UploadPool` stages each call's int64 tables through pinned lanes that are reused only
+    after the copy that last read them has completed.
+  * Support rules are small reason-returning checks (`_unsupported`, `_prefill_unsupported`);
+    a call's first sight of a (geometry, dtypes) key runs kernels and stock arithmetic side
+    by side once, and the answer is kept in `_VERDICTS` / `_PF_VERDICTS`.
+  * `_LayerGraph` owns one MoE layer's recorded decode launches and their static buffers.
+  * `_prefill_launch` splits a call whose activation or intermediate rows would not fit the
+    kernels' 32-bit row offsets into token chunks (bit-identical: a row's arithmetic does not
+    depend on the rows it shares a launch with).
+  * `install_packed_expert_kernels` is a sequence of stages (preconditions, the decode
+    verdict, per-layer prefill eligibility, the prefill verdict).
 
 Every value the stock path stores in the activation dtype is rounded to it at the same
-point, and nothing is accumulated atomically: the output is a function of (x, routing,
-weights) alone, whatever the blobs' addresses or arrival order.
-
-Without the built library (vaayu_amd/libvaayu_amd.so) the kernels raise ImportError,
-naming the file; there is no silent substitute.
+point, and nothing is accumulated atomically. Without the built library
+(vaayu_amd/libvaayu_amd.so) every kernel entry raises ImportError naming the file.
 """
 import collections
 import gc
+import itertools
 from pathlib import Path
 
 import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .block_formats import blob_layout, geom_format, FMT_E4M3, FMT_MXFP4
+from .block_formats import FMT_E4M3, FMT_MXFP4, blob_layout, geom_format
 
 try:
     _lib.load()
-    _BACKEND = _lib
+    _BACKEND, _LOAD_ERROR = _lib, None
 except ImportError as _exc:              # reported at the first kernel call / install
-    _BACKEND = None
-    _LOAD_ERROR = str(_exc)
+    _BACKEND, _LOAD_ERROR = None, str(_exc)
 
-# Truthiness of the kernel backend, under the name the engine's installer and its tests
-# use for it (they set it to None to simulate a machine without the kernels).
+# The kernel backend's truthiness under the name the engine's installer and its tests use
+# (they set it to None to stand for a machine without the kernels).
 triton = _BACKEND
 
-# relL2 of a layer's output against its reference above which a kernel is refused.
-_CHECK_TOL = 1e-2
+_CHECK_TOL = 1e-2            # relL2 of a call's output vs its reference above which: refused
 _BK_MAX = 512
-# Prefill tables group each expert's (token, slot) rows into blocks of this many rows.
-_PF_BLOCK_M = 16
+_PF_BLOCK_M = 16             # rows per block of the prefill tables
 _PF_MIN_TILE = 16
 _PF_GU_BK_MAX, _PF_DN_BK_MAX = 256, 256
 _DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 # Scale dtypes the kernels read: the activation dtypes, and E8M0 bytes (MXFP4 blobs).
 _SCALE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2, torch.uint8: 3}
 _ROLES = ("gate", "down", "up")
+# Byte span the grouped kernels address with 32-bit row offsets (activation rows x, and
+# intermediate rows h); a prefill call past it is launched in token chunks. Read at call
+# time, so a test can lower it.
+_OFFSET_LIMIT = 0xF0000000
 
 
 def _require_backend():
     if triton is None:
-        raise ImportError(globals().get("_LOAD_ERROR", "vaayu_amd kernels unavailable"))
+        raise ImportError(_LOAD_ERROR or "vaayu_amd kernels unavailable")
     return _lib.load()
 
 
-class _TableRing:
-    """Pinned host staging for the per-call pointer tables, reused round-robin
-    (vaayu/packed_expert_kernels.py:263-292). A slot's host buffer is rewritten only after
-    the copy that last read it has completed (its event); each slot has its own device
-    table, so no queued kernel's table is overwritten."""
+# ── pinned staging of the per-call tables ───────────────────────────────────────────────
 
-    def __init__(self, n_slots: int = 4):
-        self._slots: list = [None] * n_slots
-        self._next = 0
+def _pow2_at_least(n: int, floor: int = 64) -> int:
+    return max(floor, 1 << max(n - 1, 0).bit_length())
+
+
+def _same_device(a: torch.device, b) -> bool:
+    b = torch.device(b)
+    if b.type == "cuda" and b.index is None:
+        b = torch.device("cuda", torch.cuda.current_device())
+    return a == b
+
+
+class _UploadLane:
+    """One pinned int64 host buffer, its device twin, and the event recorded after the last
+    copy out of the host buffer (which must not be rewritten before that copy is done)."""
+    __slots__ = ("host", "dev", "copied", "in_flight")
+
+    def __init__(self, capacity: int, device):
+        self.host = torch.empty(capacity, dtype=torch.int64, pin_memory=True)
+        self.dev = torch.empty(capacity, dtype=torch.int64, device=device)
+        self.copied = torch.cuda.Event()
+        self.in_flight = False
+
+    def fits(self, n: int, device) -> bool:
+        return self.host.numel() >= n and _same_device(self.dev.device, device)
+
+    def upload(self, values) -> torch.Tensor:
+        n = len(values)
+        if self.in_flight:
+            self.copied.synchronize()
+        self.host[:n] = torch.as_tensor(values, dtype=torch.int64)
+        self.dev[:n].copy_(self.host[:n], non_blocking=True)
+        self.copied.record()
+        self.in_flight = True
+        return self.dev
+
+
+class _UploadPool:
+    """Round-robin lanes (vaayu/packed_expert_kernels.py:263-292 stages the same way): each
+    call's table gets its own device buffer, so a table still queued for a kernel is never
+    overwritten, and a lane's pinned buffer is reused only after its copy completed. Lanes
+    grow to the next power of two (prefill tables change length call to call)."""
+
+    def __init__(self, depth: int = 4):
+        self._slots: list = [None] * depth
+        self._turn = itertools.cycle(range(depth))
 
     def put(self, values, device) -> torch.Tensor:
-        i = self._next
-        self._next = (i + 1) % len(self._slots)
-        n = len(values)
-        slot = self._slots[i]
-        if slot is None or slot[0].numel() < n or slot[1].device != torch.device(device):
-            cap = max(64, 1 << (n - 1).bit_length())
-            host = torch.empty(cap, dtype=torch.int64, pin_memory=True)
-            slot = self._slots[i] = [host, torch.empty(cap, dtype=torch.int64, device=device),
-                                     torch.cuda.Event(), False]
-        host, dev, done, used = slot
-        if used:
-            done.synchronize()
-        host[:n] = torch.as_tensor(values, dtype=torch.int64)
-        dev[:n].copy_(host[:n], non_blocking=True)
-        done.record()
-        slot[3] = True
-        return dev
+        """A device int64 tensor whose first len(values) entries hold `values` once the
+        stream reaches this point."""
+        i = next(self._turn)
+        lane = self._slots[i]
+        if lane is None or not lane.fits(len(values), device):
+            lane = self._slots[i] = _UploadLane(_pow2_at_least(len(values)), device)
+        return lane.upload(values)
 
 
-_TABLES = _TableRing()
+_TABLES = _UploadPool()
+_PF_TABLES = _UploadPool()
 _VERDICTS: dict = {}
-_PF_TABLES = _TableRing()
 _PF_VERDICTS: dict = {}
 
 
+# ── geometry and support rules ──────────────────────────────────────────────────────────
+
 def _layout(geom) -> dict:
     """{role: (word offset, scale offset, rows, cols)} inside a blob's flat streams
-    (vaayu/packed_expert_kernels.py:301-309); FP8 / MXFP4 blobs by their own scale blocking
-    (vaayu_amd.block_formats)."""
+    (vaayu/packed_expert_kernels.py:301-309); FP8 / MXFP4 blobs by their own scale
+    blocking (vaayu_amd.block_formats)."""
     if isinstance(geom[0], str):
         return blob_layout(geom)
     bits, gs, roles = geom
-    out, w_at, s_at = {}, 0, 0
+    out, words, scales = {}, 0, 0
     for role, rows, cols in roles:
-        out[role] = (w_at, s_at, rows, cols)
-        w_at += rows * cols * bits // 32
-        s_at += rows * cols // gs
+        out[role] = (words, scales, rows, cols)
+        words += rows * cols * bits // 32
+        scales += rows * cols // gs
     return out
 
 
 def _block_k(k: int, gs: int, cap: int = _BK_MAX):
-    """Largest power-of-two multiple of the group size, at most max(cap, gs), dividing k
-    (vaayu/packed_expert_kernels.py:312-319); None if there is none."""
-    best, b = None, gs
-    while b <= max(cap, gs):
-        if k % b == 0:
-            best = b
-        b *= 2
-    return best
+    """The largest power-of-two multiple of the group size, at most max(cap, gs), that
+    divides k (vaayu/packed_expert_kernels.py:312-319); None if none does."""
+    fitting = [b for b in (gs << s for s in range(32)) if b <= max(cap, gs) and k % b == 0]
+    return fitting[-1] if fitting else None
 
 
 def _pow2_divisor(n: int, cap: int) -> int:
-    b = cap
-    while n % b:
-        b //= 2
-    return b
+    """The largest power of two at most `cap` dividing n."""
+    while n % cap:
+        cap //= 2
+    return cap
 
 
-def _unsupported(geom, act_dtype, scale_dtype, w_dtype):
-    """Why the decode kernels cannot run this geometry / these dtypes, or None.
-
-    The reference's rules (vaayu/packed_expert_kernels.py:329-346), plus what the HIP
-    GEMV needs: a row is whole 16-byte units of codes, and a unit lies in one group."""
-    shapes = {r: (rows, cols) for r, rows, cols in geom[2]}
+def _gated_mlp(geom):
+    """(intermediate, hidden) of a gate/up/down geometry, or the reason it is not one."""
+    shapes = {role: (rows, cols) for role, rows, cols in geom[2]}
     if set(shapes) != set(_ROLES):
         return f"expert roles {sorted(shapes)} are not gate/up/down"
     inter, hid = shapes["gate"]
     if shapes["up"] != (inter, hid) or shapes["down"] != (hid, inter):
         return f"projection shapes {shapes} are not a gated MLP"
+    return inter, hid
+
+
+def _first(*checks):
+    """The first reason (a non-empty string) the checks give, or None; each check is a
+    zero-argument callable, called only if every earlier one passed."""
+    for check in checks:
+        why = check()
+        if why:
+            return why
+    return None
+
+
+def _dtype_reason(**dtypes):
+    for what, dt in dtypes.items():
+        if dt not in _DTYPE_CODE:
+            return f"{what.replace('_', '-')} dtype {dt}"
+    return None
+
+
+def _unsupported(geom, act_dtype, scale_dtype, w_dtype):
+    """Why the decode kernels cannot run this geometry with these dtypes, or None.
+
+    The reference's rules (vaayu/packed_expert_kernels.py:329-346) -- a gated MLP, a
+    power-of-two group of whole words, a K tile dividing both dims, dtypes among
+    bf16/fp16/fp32 -- plus what the HIP GEMV reads: whole 16-byte units of codes, each
+    within one group."""
+    mlp = _gated_mlp(geom)
+    if isinstance(mlp, str):
+        return mlp
+    inter, hid = mlp
     if isinstance(geom[0], str):
         return _format_unsupported(geom, act_dtype, scale_dtype, w_dtype, inter, hid)
-    bits, gs, roles = geom
-    if gs & (gs - 1) or gs % (32 // bits):
-        return f"group size {gs} is not a power of two holding whole {bits}-bit words"
-    if _block_k(hid, gs) is None or _block_k(inter, gs) is None:
-        return f"no tile divides hidden {hid} / intermediate {inter} at group size {gs}"
-    for what, dt in (("activation", act_dtype), ("scale", scale_dtype),
-                     ("routing-weight", w_dtype)):
-        if dt not in _DTYPE_CODE:
-            return f"{what} dtype {dt}"
-    unit = 128 // bits                      # codes per 16-byte unit
-    if gs % unit:
-        return f"group size {gs} holds less than one 16-byte unit of {bits}-bit codes"
-    if hid % (2 * unit) or inter % unit:
-        return (f"hidden {hid} / intermediate {inter} is not whole (hidden: an even number "
-                f"of) 16-byte units of codes")
-    return None
+    bits, gs, _roles = geom
+    unit = 128 // bits                                  # codes per 16-byte unit
+    return _first(
+        lambda: (gs & (gs - 1) or gs % (32 // bits))
+        and f"group size {gs} is not a power of two holding whole {bits}-bit words",
+        lambda: (_block_k(hid, gs) is None or _block_k(inter, gs) is None)
+        and f"no tile divides hidden {hid} / intermediate {inter} at group size {gs}",
+        lambda: _dtype_reason(activation=act_dtype, scale=scale_dtype,
+                              routing_weight=w_dtype),
+        lambda: gs % unit
+        and f"group size {gs} holds less than one 16-byte unit of {bits}-bit codes",
+        lambda: (hid % (2 * unit) or inter % unit)
+        and (f"hidden {hid} / intermediate {inter} is not whole (hidden: an even number "
+             f"of) 16-byte units of codes"))
 
 
 def _format_unsupported(geom, act_dtype, scale_dtype, w_dtype, inter, hid):
@@ -167,34 +232,124 @@ def _format_unsupported(geom, act_dtype, scale_dtype, w_dtype, inter, hid):
     except (TypeError, ValueError):
         return f"code format {geom[0]!r}"
     if fmt == FMT_E4M3:
-        if scale_dtype not in _DTYPE_CODE:
-            return f"e4m3 scale dtype {scale_dtype}"
-        if group & (group - 1) or group % 16 or brows & (brows - 1) or inter % brows or hid % brows:
-            return f"e4m3 scale blocks {brows} x {group} do not tile {inter} x {hid}"
+        scale_rule = lambda: (  # noqa: E731
+            (scale_dtype not in _DTYPE_CODE and f"e4m3 scale dtype {scale_dtype}")
+            or ((group & (group - 1) or group % 16 or brows & (brows - 1) or inter % brows
+                 or hid % brows)
+                and f"e4m3 scale blocks {brows} x {group} do not tile {inter} x {hid}"))
     elif fmt == FMT_MXFP4:
-        if scale_dtype != torch.uint8:
-            return f"mxfp4 scales are E8M0 bytes, not {scale_dtype}"
+        scale_rule = lambda: (scale_dtype != torch.uint8  # noqa: E731
+                              and f"mxfp4 scales are E8M0 bytes, not {scale_dtype}")
     else:
         return f"code format {geom[0]!r}"
-    for what, dt in (("activation", act_dtype), ("routing-weight", w_dtype)):
-        if dt not in _DTYPE_CODE:
-            return f"{what} dtype {dt}"
     unit = 128 // bits
-    if hid % (2 * unit) or inter % unit or hid % group or inter % group:
-        return f"hidden {hid} / intermediate {inter} is not whole 16-byte units and scale groups"
-    return None
+    return _first(
+        scale_rule,
+        lambda: _dtype_reason(activation=act_dtype, routing_weight=w_dtype),
+        lambda: (hid % (2 * unit) or inter % unit or hid % group or inter % group)
+        and f"hidden {hid} / intermediate {inter} is not whole 16-byte units and scale groups")
 
+
+def _prefill_unsupported(geom, act_dtype, scale_dtype, w_dtype):
+    """Why the grouped prefill kernels cannot run this geometry, or None
+    (vaayu/packed_expert_kernels.py:657-673): the decode rules, no fp32 activations, and
+    an MFMA K step -- 4 lanes' 16-byte units -- that divides hidden and intermediate."""
+    why = _unsupported(geom, act_dtype, scale_dtype, w_dtype)
+    if why:
+        return why
+    if act_dtype == torch.float32:
+        return "fp32 activations (the matrix cores would run them at reduced precision)"
+    lay = _layout(geom)
+    dims = (("hidden", lay["gate"][3]), ("intermediate", lay["gate"][2]))
+    if isinstance(geom[0], str):                 # FP8 e4m3 / MXFP4 blobs
+        step = 4 * (128 // geom_format(geom)[1])
+        return _first(*(lambda what=what, k=k: k % step
+                        and f"{what} {k} is not a multiple of the {step}-code K tile"
+                        for what, k in dims))
+    bits, gs, _roles = geom
+    if bits not in (4, 8):
+        return f"{bits}-bit codes (the grouped kernels take 4 and 8)"
+    step = 4 * (128 // bits)
+    tile_cap = min(_PF_GU_BK_MAX, _PF_DN_BK_MAX)
+
+    def k_rules(what, k):
+        return (lambda: _block_k(k, gs, tile_cap) // (32 // bits) < _PF_MIN_TILE
+                and f"{what} {k} at group size {gs} leaves a K tile under {_PF_MIN_TILE} words",
+                lambda: k % step and f"{what} {k} is not a multiple of the {step}-code K tile")
+    return _first(*(rule for what, k in dims for rule in k_rules(what, k)))
+
+
+def _aligned(blobs) -> bool:
+    """The kernels read codes with 16-byte loads: every packed stream must start on 16 B."""
+    return all(b["flat"]["packed"].data_ptr() % 16 == 0 for b in blobs)
+
+
+def _kernel_ready(blobs) -> bool:
+    """The entries are blobs of ONE geometry, each aligned for the kernels' loads."""
+    blobs = list(blobs)
+    geoms = {b.get("geom") for b in blobs}
+    return len(geoms) == 1 and None not in geoms and _aligned(blobs)
+
+
+def _scale_code(blob) -> int:
+    return _SCALE_CODE[blob["flat"]["scale"].dtype]
+
+
+# ── verdicts: kernels against the stock arithmetic, once per key ─────────────────────────
+
+_REFERENCE = {"decode": "the stock per-expert loop",
+              "prefill": "the per-expert loop with fp32-summed GEMMs"}
+
+
+def _disagreement(x, fill_reference, fill_candidate, kind):
+    """Why the candidate's fp32 output (relL2) does not match the reference's on this call,
+    or None. A failed launch is a disagreement too."""
+    try:
+        want = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        got = torch.empty_like(want)
+        fill_reference(want)
+        fill_candidate(got)
+        err = ((got - want).norm() / want.norm().clamp_min(1e-30)).item()
+    except Exception as exc:  # a rejected or failed launch
+        return f"{type(exc).__name__}: {exc}"
+    if err <= _CHECK_TOL:                 # False for NaN: a NaN output is refused
+        return None
+    return f"relL2 {err:.2e} vs {_REFERENCE[kind]}, tolerance {_CHECK_TOL:.0e}"
+
+
+def _judge(kind, x, why, fill_reference, fill_candidate) -> bool:
+    """The verdict on one call (vaayu/packed_expert_kernels.py:413-433): True if the
+    kernels may run it. A refusal prints one WARNING naming `kind`; a missing kernel
+    library is not a refusal, it raises."""
+    if why is None:
+        _require_backend()
+        why = _disagreement(x, fill_reference, fill_candidate, kind)
+    if why is not None:
+        print(f"[Vaayu] WARNING: fused packed-expert {kind} kernel refused ({why}); "
+              f"these experts stay on the stock per-expert path")
+    return why is None
+
+
+def _remembered(book_name: str, key, decide) -> bool:
+    """The verdict kept in the module dict `book_name` for `key`, decided on first sight.
+    The dict is looked up by name at call time (tests swap in fresh ones)."""
+    book = globals()[book_name]
+    if key not in book:
+        book[key] = decide()
+    return book[key]
+
+
+def _verdict_key(blob, x, routing_weights):
+    return (blob["geom"], x.dtype, routing_weights.dtype, blob["flat"]["scale"].dtype)
+
+
+# ── decode ──────────────────────────────────────────────────────────────────────────────
 
 def _table_values(pairs) -> list:
-    """The pointer table, flattened: (packed address, scale address, slot) per pair
+    """The decode pointer table, flattened: (packed address, scale address, slot) per pair
     (vaayu/packed_expert_kernels.py:349-352)."""
     return [v for blob, slot in pairs
             for v in (blob["flat"]["packed"].data_ptr(), blob["flat"]["scale"].data_ptr(), slot)]
-
-
-def _aligned(pairs_or_blobs) -> bool:
-    """The kernels read codes with 16-byte loads: every packed stream must start on 16 B."""
-    return all(b["flat"]["packed"].data_ptr() % 16 == 0 for b in pairs_or_blobs)
 
 
 def _gate_up(x, tbl, n, geom, sc, h=None):
@@ -205,98 +360,70 @@ def _gate_up(x, tbl, n, geom, sc, h=None):
     g = _lib.geom_struct(geom)
     if h is None:
         h = torch.empty(n, g.inter, dtype=x.dtype, device=x.device)
-    rc = lib.vaayu_decode_gate_up(x.data_ptr(), tbl.data_ptr(), h.data_ptr(), n, g,
-                                  _DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device))
-    _lib.check(rc, "vaayu_decode_gate_up")
+    _lib.check(lib.vaayu_decode_gate_up(x.data_ptr(), tbl.data_ptr(), h.data_ptr(), n, g,
+                                        _DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device)),
+               "vaayu_decode_gate_up")
     return h
 
 
+def _rounds_weighted(weight_dtype, act_dtype) -> bool:
+    """torch promotes `y * w` to fp32 unless the weight is already the (half-precision)
+    activation dtype; only then does the product round."""
+    return weight_dtype == act_dtype and act_dtype != torch.float32
+
+
 def _down(h, tbl, routing_weights, out, n, geom, sc) -> None:
-    """`out` = the fp32 sum, in table order, of each row's down projection times its
-    weight (vaayu/packed_expert_kernels.py:374-387). torch promotes `y * w` to fp32 unless
-    the weight is already the activation dtype; only then does the product round."""
+    """`out` = the fp32 sum, in table order, of each row's down projection times its weight
+    (vaayu/packed_expert_kernels.py:374-387)."""
     lib = _require_backend()
-    g = _lib.geom_struct(geom)
-    rw = routing_weights.reshape(-1)
-    if not rw.is_contiguous():
-        rw = rw.contiguous()
-    w_round = rw.dtype == h.dtype and h.dtype != torch.float32
-    rc = lib.vaayu_decode_down(h.data_ptr(), tbl.data_ptr(), rw.data_ptr(), _DTYPE_CODE[rw.dtype],
-                               out.data_ptr(), n, g, _DTYPE_CODE[h.dtype], sc, int(w_round),
-                               _lib.stream_ptr(h.device))
-    _lib.check(rc, "vaayu_decode_down")
+    rw = routing_weights.reshape(-1).contiguous()
+    _lib.check(lib.vaayu_decode_down(h.data_ptr(), tbl.data_ptr(), rw.data_ptr(),
+                                     _DTYPE_CODE[rw.dtype], out.data_ptr(), n,
+                                     _lib.geom_struct(geom), _DTYPE_CODE[h.dtype], sc,
+                                     int(_rounds_weighted(rw.dtype, h.dtype)),
+                                     _lib.stream_ptr(h.device)),
+               "vaayu_decode_down")
 
 
 def _launch(x, pairs, routing_weights, out) -> None:
-    """The two decode kernels over `pairs`, into `out`. No checks: `_checked` gates this
-    (vaayu/packed_expert_kernels.py:390-396)."""
-    geom = pairs[0][0]["geom"]
-    sc = _SCALE_CODE[pairs[0][0]["flat"]["scale"].dtype]
+    """Both decode kernels over `pairs`, into `out`, unchecked (`_checked` gates this;
+    vaayu/packed_expert_kernels.py:390-396)."""
+    blob = pairs[0][0]
     tbl = _TABLES.put(_table_values(pairs), x.device)
-    h = _gate_up(x, tbl, len(pairs), geom, sc)
-    _down(h, tbl, routing_weights, out, len(pairs), geom, sc)
+    h = _gate_up(x, tbl, len(pairs), blob["geom"], _scale_code(blob))
+    _down(h, tbl, routing_weights, out, len(pairs), blob["geom"], _scale_code(blob))
 
 
 def stock_experts_decode(x, pairs, routing_weights, out, act_fn) -> None:
-    """The per-slot loop's arithmetic for one token, pair by pair, into `out`: the
-    reference the kernels are held to and their fallback (vaayu/packed_expert_kernels.py:
-    399-410) -- dense weights, three `F.linear`, `act_fn`, the routing-weight product with
-    torch's promotion, an fp32 add in pair order."""
+    """One token through the per-slot loop's arithmetic, into `out`: the reference the
+    kernels are held to and their fallback (vaayu/packed_expert_kernels.py:399-410) --
+    dense weights, three `F.linear`, `act_fn`, the routing-weight product with torch's
+    promotion, an fp32 add in pair order."""
     from .moe_patch import expert_weights_from_entry
     rw = routing_weights.reshape(-1)
     out.zero_()
     for blob, slot in pairs:
-        w_gate, w_down, w_up = expert_weights_from_entry(blob, x.dtype)
-        y = F.linear(act_fn(F.linear(x, w_gate)) * F.linear(x, w_up), w_down)
-        out += (y * rw[slot:slot + 1]).to(out.dtype)
-
-
-_REFERENCE = {"decode": "the stock per-expert loop",
-              "prefill": "the per-expert loop with fp32-summed GEMMs"}
-
-
-def _agrees(why, x, run_stock, run_kernel, what) -> bool:
-    """True if the kernel agrees (relL2 <= _CHECK_TOL) with its reference on this call's
-    data (vaayu/packed_expert_kernels.py:413-433). A refusal prints one WARNING naming
-    `what`. A missing kernel library is not a disagreement: it raises."""
-    if why is None:
-        _require_backend()
-        try:
-            ref = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-            got = torch.empty_like(ref)
-            run_stock(ref)
-            run_kernel(got)
-            err = ((got - ref).norm() / ref.norm().clamp_min(1e-30)).item()
-            if not err <= _CHECK_TOL:
-                why = (f"relL2 {err:.2e} vs {_REFERENCE[what]}, "
-                       f"tolerance {_CHECK_TOL:.0e}")
-        except Exception as exc:  # a rejected or failed launch
-            why = f"{type(exc).__name__}: {exc}"
-    if why is None:
-        return True
-    print(f"[Vaayu] WARNING: fused packed-expert {what} kernel refused ({why}); "
-          f"these experts stay on the stock per-expert path")
-    return False
+        gate_w, down_w, up_w = expert_weights_from_entry(blob, x.dtype)
+        hidden = act_fn(F.linear(x, gate_w)) * F.linear(x, up_w)
+        out += (F.linear(hidden, down_w) * rw[slot:slot + 1]).to(out.dtype)
 
 
 def _verdict(x, pairs, routing_weights, act_fn) -> bool:
-    """Run the kernels AND the stock arithmetic on this call's data; True if they agree
+    """Kernels AND stock arithmetic on this call's data; True if they agree
     (vaayu/packed_expert_kernels.py:440-447)."""
     blob = pairs[0][0]
-    why = _unsupported(blob["geom"], x.dtype, blob["flat"]["scale"].dtype, routing_weights.dtype)
-    return _agrees(why, x,
-                   lambda ref: stock_experts_decode(x, pairs, routing_weights, ref, act_fn),
-                   lambda got: _launch(x, pairs, routing_weights, got), "decode")
+    return _judge("decode", x,
+                  _unsupported(blob["geom"], x.dtype, blob["flat"]["scale"].dtype,
+                               routing_weights.dtype),
+                  lambda want: stock_experts_decode(x, pairs, routing_weights, want, act_fn),
+                  lambda got: _launch(x, pairs, routing_weights, got))
 
 
 def _checked(x, pairs, routing_weights, act_fn) -> bool:
-    """The cached verdict for this call's (geometry, dtypes) key, taken on first sight
-    (vaayu/packed_expert_kernels.py:450-456)."""
-    blob = pairs[0][0]
-    key = (blob["geom"], x.dtype, routing_weights.dtype, blob["flat"]["scale"].dtype)
-    if key not in _VERDICTS:
-        _VERDICTS[key] = _verdict(x, pairs, routing_weights, act_fn)
-    return _VERDICTS[key]
+    """The verdict of this call's (geometry, dtypes) key (vaayu/packed_expert_kernels.py:
+    450-456)."""
+    return _remembered("_VERDICTS", _verdict_key(pairs[0][0], x, routing_weights),
+                       lambda: _verdict(x, pairs, routing_weights, act_fn))
 
 
 def packed_experts_decode(x, pairs, routing_weights, out, act_fn) -> None:
@@ -310,229 +437,212 @@ def packed_experts_decode(x, pairs, routing_weights, out, act_fn) -> None:
     act_fn          the experts' activation; only the stock fallback calls it
 
     Entries that are not all blobs of ONE geometry run the stock arithmetic."""
-    geoms = {blob.get("geom") for blob, _slot in pairs}
-    if len(geoms) != 1 or None in geoms or not _aligned(b for b, _s in pairs):
-        stock_experts_decode(x, pairs, routing_weights, out, act_fn)
-    elif _checked(x, pairs, routing_weights, act_fn):
+    on_kernels = (_kernel_ready(b for b, _slot in pairs)
+                  and _checked(x, pairs, routing_weights, act_fn))
+    if on_kernels:
         _launch(x, pairs, routing_weights, out)
     else:
         stock_experts_decode(x, pairs, routing_weights, out, act_fn)
 
 
-# ── the decode kernels of one MoE layer as ONE graph (vaayu/packed_expert_kernels.py:483-654)
-# A decode visit's inputs (x, the routing weights, the shared expert's output) are the same
-# tensors every token under the engine's decode graphs, so the table upload, both launches
-# and the epilogue are recorded once per layer and replayed with only the table's contents
-# rewritten. Each capture is held bitwise to the eager launch.
+# ── one MoE layer's decode launches as ONE graph (vaayu/packed_expert_kernels.py:483-654) ──
+# Under the engine's decode graphs a layer's inputs (x, the routing weights, the shared
+# expert's output) are the same tensors every token, so the table upload, both launches
+# and the epilogue are recorded once per layer and replayed with only the pinned table
+# rewritten. Each recording is held bitwise to the eager launch before it is kept.
 _GRAPHS: dict = {}              # layer -> _LayerGraph
 _GRAPH_REFUSED: dict = {}       # layer -> why
 _GRAPH_WARNED: set = set()
-_GRAPH_STREAMS: dict = {}       # device -> the capture stream
+_GRAPH_STREAMS: dict = {}       # device -> the recording stream
 GRAPH_STATS: collections.Counter = collections.Counter()
-
-
-class _LayerGraph:
-    __slots__ = ("key", "graph", "host", "host_np", "tbl", "h", "out", "tmp", "result",
-                 "done", "replays")
 
 
 def _tail(out, dtype, shared):
     """The fused forward's epilogue: the fp32 sum cast back, plus the shared expert."""
     result = out.to(dtype)
-    if shared is not None:
-        result = result + shared.to(result.dtype)
-    return result
+    return result + shared.to(result.dtype) if shared is not None else result
+
+
+def _warn_once(why, message) -> None:
+    if why not in _GRAPH_WARNED:
+        _GRAPH_WARNED.add(why)
+        print(message)
 
 
 def _refuse_graph(layer, why) -> None:
     _GRAPH_REFUSED[layer] = why
     _GRAPHS.pop(layer, None)
     GRAPH_STATS["refused"] += 1
-    if why not in _GRAPH_WARNED:
-        _GRAPH_WARNED.add(why)
-        print(f"[Vaayu] WARNING: packed-expert decode graph refused for MoE layer {layer} "
-              f"({why}); it launches eagerly. Later layers refused for the same reason are "
-              f"not listed.")
+    _warn_once(why, f"[Vaayu] WARNING: packed-expert decode graph refused for MoE layer "
+                    f"{layer} ({why}); it launches eagerly. Later layers refused for the same "
+                    f"reason are not listed.")
 
 
 def _warn_skip(why) -> None:
     """A call the graph cannot take launches eagerly; said once per reason."""
-    if why not in _GRAPH_WARNED:
-        _GRAPH_WARNED.add(why)
-        print(f"[Vaayu] WARNING: packed-expert decode graph not used ({why}); those calls "
-              f"launch the kernels eagerly. Shown once per reason.")
+    _warn_once(why, f"[Vaayu] WARNING: packed-expert decode graph not used ({why}); those "
+                    f"calls launch the kernels eagerly. Shown once per reason.")
+
+
+def _release_pool(pool) -> None:
+    """Return a graph pool whose recording failed to end: torch's allocator otherwise keeps
+    believing a capture records into it."""
+    dev = torch.cuda.current_device()
+    for release in (torch._C._cuda_endAllocateToPool, torch._C._cuda_releasePool):
+        try:
+            release(dev, pool)
+        except Exception:
+            pass
+
+
+class _LayerGraph:
+    """One MoE layer's recorded decode: the pinned table it replays from (`host`), its
+    device copy (`tbl`), the static intermediates (`h`, `out`, `tmp`) and the returned
+    tensor (`result`, or `out` without the epilogue)."""
+    __slots__ = ("key", "graph", "host", "host_np", "tbl", "h", "out", "tmp", "result",
+                 "done", "replays")
+
+    def __init__(self, key, n_values, n_pairs, inter, x, tail, shared):
+        dev = x.device
+        self.key, self.replays, self.graph = key, 0, None
+        self.host = torch.empty(n_values, dtype=torch.int64, pin_memory=True)
+        self.host_np = self.host.numpy()
+        self.tbl = torch.empty(n_values, dtype=torch.int64, device=dev)
+        self.h = torch.empty(n_pairs, inter, dtype=x.dtype, device=dev)
+        self.out = torch.empty(x.shape, dtype=torch.float32, device=dev)
+        self.tmp = torch.empty(x.shape, dtype=x.dtype, device=dev) if tail else None
+        self.result = (torch.empty(x.shape, dtype=x.dtype, device=dev)
+                       if tail and shared is not None else self.tmp)
+        self.done = torch.cuda.Event()
+
+    def returned(self, tail):
+        return self.result if tail else self.out
+
+    def record(self, x, routing_weights, shared, tail, geom, sc) -> None:
+        """Capture the launches on the device's recording stream (no allocation inside)."""
+        n = self.h.shape[0]
+        graph, pool = torch.cuda.CUDAGraph(), torch.cuda.graph_pool_handle()
+        dev = x.device
+        side = _GRAPH_STREAMS.get(dev)
+        if side is None:
+            side = _GRAPH_STREAMS[dev] = torch.cuda.Stream(device=dev)
+        here = torch.cuda.current_stream(dev)
+        side.wait_stream(here)
+        with torch.cuda.stream(side), torch.no_grad():
+            graph.capture_begin(pool=pool, capture_error_mode="thread_local")
+            try:
+                self.tbl.copy_(self.host, non_blocking=True)
+                _gate_up(x, self.tbl, n, geom, sc, h=self.h)
+                _down(self.h, self.tbl, routing_weights, self.out, n, geom, sc)
+                if tail:
+                    self.tmp.copy_(self.out)
+                    if shared is not None:
+                        torch.add(self.tmp, shared, out=self.result)
+            finally:
+                try:
+                    graph.capture_end()
+                except Exception:
+                    _release_pool(pool)
+                    raise
+        here.wait_stream(side)
+        self.graph = graph
+
+    def replay(self, values) -> None:
+        self.done.synchronize()             # the previous replay has read the table
+        self.host_np[:] = values
+        self.graph.replay()
+        self.done.record()
+        self.replays += 1
+
+
+def _graph_obstacle(x, pairs, routing_weights, shared, tail):
+    """(reason, say_it) when the graph cannot take this call: say_it is False for calls that
+    are simply not the graph's (mixed or unaligned entries), True for inputs it cannot bind."""
+    if not _kernel_ready(b for b, _s in pairs):
+        return "not one geometry of aligned blobs", False
+    if not (x.is_contiguous() and routing_weights.is_contiguous()):
+        return "a non-contiguous expert input or routing-weight tensor", True
+    if tail and shared is not None and shared.dtype != x.dtype:
+        return f"the shared expert's output is {shared.dtype}, the activations {x.dtype}", True
+    return None, False
 
 
 def packed_experts_decode_graphed(layer, x, pairs, routing_weights, shared, act_fn, tail):
     """`packed_experts_decode` (and, `tail` True, the forward's epilogue) through one graph
     per MoE layer -- or None: not the graph's call, run the eager path
-    (vaayu/packed_expert_kernels.py:531-575). Returns a STATIC tensor the layer's next
-    call overwrites: the fp32 sum [1, hidden], or `_tail(sum, x.dtype, shared)`."""
+    (vaayu/packed_expert_kernels.py:531-575). Returns a STATIC tensor the layer's next call
+    overwrites: the fp32 sum [1, hidden], or `_tail(sum, x.dtype, shared)`."""
     if layer in _GRAPH_REFUSED:
         return None
-    blob0 = pairs[0][0]
-    geom = blob0.get("geom")
-    if geom is None or any(blob.get("geom") != geom for blob, _slot in pairs[1:]):
-        return None
-    if not _aligned(b for b, _s in pairs):
-        return None
-    if not (x.is_contiguous() and routing_weights.is_contiguous()):
-        _warn_skip("a non-contiguous expert input or routing-weight tensor")
-        return None
-    if tail and shared is not None and shared.dtype != x.dtype:
-        _warn_skip(f"the shared expert's output is {shared.dtype}, the activations {x.dtype}")
+    why, say_it = _graph_obstacle(x, pairs, routing_weights, shared, tail)
+    if why is not None:
+        if say_it:
+            _warn_skip(why)
         return None
     if not _checked(x, pairs, routing_weights, act_fn):
         return None
-    vals = _table_values(pairs)
+    blob = pairs[0][0]
+    values = _table_values(pairs)
     key = (len(pairs), x.data_ptr(), routing_weights.data_ptr(), routing_weights.dtype,
-           0 if shared is None else shared.data_ptr(), tail, geom, x.dtype,
-           blob0["flat"]["scale"].dtype)
-    g = _GRAPHS.get(layer)
-    if g is not None and g.key == key:
-        g.done.synchronize()            # the last replay has read the table
-        g.host_np[:] = vals
-        g.graph.replay()
-        g.done.record()
-        g.replays += 1
+           0 if shared is None else shared.data_ptr(), tail, blob["geom"], x.dtype,
+           blob["flat"]["scale"].dtype)
+    kept = _GRAPHS.get(layer)
+    if kept is not None and kept.key == key:
+        kept.replay(values)
         GRAPH_STATS["replays"] += 1
-        return g.result if tail else g.out
-    if g is not None:
+        return kept.returned(tail)
+    if kept is not None:                    # inputs moved: this layer records again
         del _GRAPHS[layer]
-        if g.replays == 0:
+        if kept.replays == 0:
             GRAPH_STATS["replaced_unreplayed"] += 1
-        del g
-    return _capture(layer, key, x, pairs, routing_weights, shared, tail, vals, act_fn)
+        del kept
+    return _record_layer(layer, key, x, pairs, routing_weights, shared, tail, values)
 
 
-def _cleanup_pool(pool) -> None:
-    """Release a graph pool whose capture failed to end: torch's allocator otherwise
-    keeps believing a capture records into it."""
-    dev = torch.cuda.current_device()
+def _record_layer(layer, key, x, pairs, routing_weights, shared, tail, values):
+    """Launch eagerly, record the layer's graph, replay it once and keep it only if the
+    replay equals the eager result bit for bit (vaayu/packed_expert_kernels.py:578-654).
+    The eager result is what this call returns unless the graph's equals it; nothing here
+    raises into the request."""
+    blob = pairs[0][0]
+    eager_out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    _launch(x, pairs, routing_weights, eager_out)
+    eager = _tail(eager_out, x.dtype, shared) if tail else eager_out
+    collecting = gc.isenabled()
+    gc.disable()            # a collection inside the capture could free a tensor mid-record
     try:
-        torch._C._cuda_endAllocateToPool(dev, pool)
-    except Exception:
-        pass
-    try:
-        torch._C._cuda_releasePool(dev, pool)
-    except Exception:
-        pass
-
-
-def _capture(layer, key, x, pairs, rw, shared, tail, vals, act_fn):
-    """Record the layer's graph, replay it once and hold it bitwise to the eager launch
-    (vaayu/packed_expert_kernels.py:578-654). Nothing here raises into the request."""
-    geom = pairs[0][0]["geom"]
-    sc = _SCALE_CODE[pairs[0][0]["flat"]["scale"].dtype]
-    n = len(pairs)
-    inter = _layout(geom)["gate"][2]
-    dev = x.device
-    ref_out = torch.empty(x.shape, dtype=torch.float32, device=dev)
-    _launch(x, pairs, rw, ref_out)
-    ref = _tail(ref_out, x.dtype, shared) if tail else ref_out
-    g = _LayerGraph()
-    graph = torch.cuda.CUDAGraph()
-    pool = torch.cuda.graph_pool_handle()
-    was = gc.isenabled()
-    gc.disable()
-    try:
-        g.key, g.replays = key, 0
-        g.host = torch.empty(len(vals), dtype=torch.int64, pin_memory=True)
-        g.host_np = g.host.numpy()
-        g.host_np[:] = vals
-        g.tbl = torch.empty(len(vals), dtype=torch.int64, device=dev)
-        g.h = torch.empty(n, inter, dtype=x.dtype, device=dev)
-        g.out = torch.empty(x.shape, dtype=torch.float32, device=dev)
-        g.tmp = torch.empty(x.shape, dtype=x.dtype, device=dev) if tail else None
-        g.result = (torch.empty(x.shape, dtype=x.dtype, device=dev)
-                    if tail and shared is not None else g.tmp)
-        g.done = torch.cuda.Event()
-        side = _GRAPH_STREAMS.get(dev)
-        if side is None:
-            side = _GRAPH_STREAMS[dev] = torch.cuda.Stream(device=dev)
-        cur = torch.cuda.current_stream(dev)
-        side.wait_stream(cur)
-        with torch.cuda.stream(side), torch.no_grad():
-            graph.capture_begin(pool=pool, capture_error_mode="thread_local")
-            try:
-                g.tbl.copy_(g.host, non_blocking=True)
-                _gate_up(x, g.tbl, n, geom, sc, h=g.h)
-                _down(g.h, g.tbl, rw, g.out, n, geom, sc)
-                if tail:
-                    g.tmp.copy_(g.out)
-                    if shared is not None:
-                        torch.add(g.tmp, shared, out=g.result)
-            finally:
-                try:
-                    graph.capture_end()
-                except Exception:
-                    _cleanup_pool(pool)
-                    raise
-        cur.wait_stream(side)
-        g.graph = graph
-        graph.replay()
-        got = g.result if tail else g.out
-        same = torch.equal(got, ref)
+        g = _LayerGraph(key, len(values), len(pairs), _layout(blob["geom"])["gate"][2], x,
+                        tail, shared)
+        g.host_np[:] = values
+        g.record(x, routing_weights, shared, tail, blob["geom"], _scale_code(blob))
+        g.graph.replay()
+        agrees = torch.equal(g.returned(tail), eager)
     except Exception as exc:
         first = (str(exc).splitlines() or [""])[0][:200]
         _refuse_graph(layer, f"capture failed: {type(exc).__name__}: {first}")
-        return ref
+        return eager
     finally:
-        if was:
+        if collecting:
             gc.enable()
-    if not same:
+    if not agrees:
         _refuse_graph(layer, "its replay disagrees bitwise with the eager launch")
-        return ref
+        return eager
     g.done.record()
     _GRAPHS[layer] = g
     GRAPH_STATS["captures"] += 1
-    return got
+    return g.returned(tail)
 
 
 # ── prefill ─────────────────────────────────────────────────────────────────────────────
 
-def _prefill_unsupported(geom, act_dtype, scale_dtype, w_dtype):
-    """Why the grouped prefill kernels cannot run this geometry, or None
-    (vaayu/packed_expert_kernels.py:657-673): the decode rules, no fp32 activations, and
-    an MFMA K step -- 4 lanes' 16-byte units -- that divides hidden and intermediate."""
-    why = _unsupported(geom, act_dtype, scale_dtype, w_dtype)
-    if why is not None:
-        return why
-    if isinstance(geom[0], str):                 # FP8 e4m3 / MXFP4 blobs
-        if act_dtype == torch.float32:
-            return "fp32 activations (the matrix cores would run them at reduced precision)"
-        _fmt, bits, _group, _brows = geom_format(geom)
-        lay = _layout(geom)
-        step = 4 * (128 // bits)
-        for what, k in (("hidden", lay["gate"][3]), ("intermediate", lay["gate"][2])):
-            if k % step:
-                return f"{what} {k} is not a multiple of the {step}-code K tile"
-        return None
-    bits, gs, _roles = geom
-    lay = _layout(geom)
-    inter, hid = lay["gate"][2], lay["gate"][3]
-    if act_dtype == torch.float32:
-        return "fp32 activations (the matrix cores would run them at reduced precision)"
-    if bits not in (4, 8):
-        return f"{bits}-bit codes (the grouped kernels take 4 and 8)"
-    step = 4 * (128 // bits)
-    for what, k in (("hidden", hid), ("intermediate", inter)):
-        if _block_k(k, gs, min(_PF_GU_BK_MAX, _PF_DN_BK_MAX)) // (32 // bits) < _PF_MIN_TILE:
-            return f"{what} {k} at group size {gs} leaves a K tile under {_PF_MIN_TILE} words"
-        if k % step:
-            return f"{what} {k} is not a multiple of the {step}-code K tile"
-    return None
-
-
 def _prefill_plan(eidx_cpu):
     """(order, live, counts) of one call's routing (vaayu/packed_expert_kernels.py:676-688):
-    row ids (token*top_k + slot) stable-sorted by expert id, the routed ids ascending,
-    and rows per routed expert."""
-    eids = eidx_cpu.reshape(-1)
-    order = torch.argsort(eids, stable=True)
-    per_expert = torch.bincount(eids)
-    live = per_expert.nonzero().reshape(-1)
-    return order, live, per_expert[live]
+    row ids (token*top_k + slot) stable-sorted by expert id, the routed ids ascending, and
+    the rows of each."""
+    flat = eidx_cpu.reshape(-1)
+    rows_per_expert = torch.bincount(flat)
+    live = torch.nonzero(rows_per_expert).reshape(-1)
+    return torch.argsort(flat, stable=True), live, rows_per_expert[live]
 
 
 def _prefill_tables(eidx_cpu, plan, blobs, device):
@@ -540,28 +650,27 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     (vaayu/packed_expert_kernels.py:691-717): (tbl, rows, ord, n_blocks).
 
     tbl   [n_blocks, 2] (packed address, scale address) of each block's expert
-    rows  [n_blocks, _PF_BLOCK_M] row ids, each expert's run padded to whole blocks with -1
+    rows  [n_blocks, _PF_BLOCK_M] row ids, each expert's rows padded to whole blocks with -1
     ord   [tokens, top_k] row ids of each token's slots in ascending expert id"""
     order, live, counts = plan
-    n, top_k = eidx_cpu.shape
-    nblk = (counts + _PF_BLOCK_M - 1) // _PF_BLOCK_M
-    blk_end = nblk.cumsum(0)
-    n_blocks = int(blk_end[-1])
-    owner = torch.repeat_interleave(torch.arange(live.numel()), counts)
-    first_row = counts.cumsum(0) - counts
-    dest = (((blk_end - nblk) * _PF_BLOCK_M)[owner] + torch.arange(order.numel())
-            - first_row[owner])
+    tokens, top_k = eidx_cpu.shape
+    blocks = (counts + _PF_BLOCK_M - 1) // _PF_BLOCK_M          # per live expert
+    n_blocks = int(blocks.sum())
+    expert_of_row = torch.repeat_interleave(torch.arange(live.numel()), counts)
+    # a row's place: its expert's first padded slot plus its rank among that expert's rows
+    padded_start = (torch.cumsum(blocks, 0) - blocks) * _PF_BLOCK_M
+    rank = torch.arange(order.numel()) - (torch.cumsum(counts, 0) - counts)[expert_of_row]
     rows = torch.full((n_blocks * _PF_BLOCK_M,), -1, dtype=torch.int64)
-    rows[dest] = order
-    ptrs = torch.tensor([(blobs[e]["flat"]["packed"].data_ptr(),
-                          blobs[e]["flat"]["scale"].data_ptr()) for e in live.tolist()],
-                        dtype=torch.int64)
-    tbl = ptrs[torch.repeat_interleave(torch.arange(live.numel()), nblk)].reshape(-1)
-    slot_order = (torch.argsort(eidx_cpu, dim=1, stable=True)
-                  + (torch.arange(n) * top_k)[:, None]).reshape(-1)
-    dev = _PF_TABLES.put(torch.cat([tbl, rows, slot_order]), device)
+    rows[padded_start[expert_of_row] + rank] = order
+    addresses = torch.tensor([[blobs[e]["flat"]["packed"].data_ptr(),
+                               blobs[e]["flat"]["scale"].data_ptr()] for e in live.tolist()],
+                             dtype=torch.int64)
+    tbl = torch.repeat_interleave(addresses, blocks, dim=0).reshape(-1)
+    by_expert = torch.argsort(eidx_cpu, dim=1, stable=True)
+    ord_ = (by_expert + top_k * torch.arange(tokens)[:, None]).reshape(-1)
+    dev = _PF_TABLES.put(torch.cat([tbl, rows, ord_]), device)
     a, b = tbl.numel(), tbl.numel() + rows.numel()
-    return dev[:a], dev[a:b], dev[b:b + slot_order.numel()], n_blocks
+    return dev[:a], dev[a:b], dev[b:b + ord_.numel()], n_blocks
 
 
 def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None):
@@ -571,10 +680,10 @@ def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None):
     g = _lib.geom_struct(geom)
     if h is None:
         h = torch.empty(x.shape[0] * top_k, g.inter, dtype=x.dtype, device=x.device)
-    rc = lib.vaayu_prefill_gate_up(x.data_ptr(), rows.data_ptr(), tbl.data_ptr(), h.data_ptr(),
-                                   n_blocks, top_k, g, _DTYPE_CODE[x.dtype], sc,
-                                   _lib.stream_ptr(x.device))
-    _lib.check(rc, "vaayu_prefill_gate_up")
+    _lib.check(lib.vaayu_prefill_gate_up(x.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
+                                         h.data_ptr(), n_blocks, top_k, g,
+                                         _DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device)),
+               "vaayu_prefill_gate_up")
     return h
 
 
@@ -586,11 +695,12 @@ def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None):
     rw = routing_weights.reshape(-1).contiguous()
     if y is None:
         y = torch.empty(h.shape[0], g.hidden, dtype=torch.float32, device=h.device)
-    w_round = rw.dtype == h.dtype and h.dtype != torch.float32
-    rc = lib.vaayu_prefill_down(h.data_ptr(), rows.data_ptr(), tbl.data_ptr(), rw.data_ptr(),
-                                _DTYPE_CODE[rw.dtype], y.data_ptr(), n_blocks, g,
-                                _DTYPE_CODE[h.dtype], sc, int(w_round), _lib.stream_ptr(h.device))
-    _lib.check(rc, "vaayu_prefill_down")
+    _lib.check(lib.vaayu_prefill_down(h.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
+                                      rw.data_ptr(), _DTYPE_CODE[rw.dtype], y.data_ptr(),
+                                      n_blocks, g, _DTYPE_CODE[h.dtype], sc,
+                                      int(_rounds_weighted(rw.dtype, h.dtype)),
+                                      _lib.stream_ptr(h.device)),
+               "vaayu_prefill_down")
     return y
 
 
@@ -598,29 +708,55 @@ def _reduce(y, order, out, top_k) -> None:
     """`out` [tokens, hidden] fp32 = each token's contributions summed in `order`
     (vaayu/packed_expert_kernels.py:752-757)."""
     lib = _require_backend()
-    rc = lib.vaayu_prefill_reduce(y.data_ptr(), order.data_ptr(), out.data_ptr(), out.shape[0],
-                                  top_k, y.shape[1], _lib.stream_ptr(y.device))
-    _lib.check(rc, "vaayu_prefill_reduce")
+    _lib.check(lib.vaayu_prefill_reduce(y.data_ptr(), order.data_ptr(), out.data_ptr(),
+                                        out.shape[0], top_k, y.shape[1],
+                                        _lib.stream_ptr(y.device)),
+               "vaayu_prefill_reduce")
 
 
-def _prefill_launch(x, eidx_cpu, routing_weights, blobs, out, plan=None) -> None:
-    """The three prefill kernels over one call. No checks: `_prefill_checked` gates this
-    (vaayu/packed_expert_kernels.py:760-777). A strided `x` is made dense first; a
-    strided `out` is written through a dense temporary."""
-    plan = plan or _prefill_plan(eidx_cpu)
+def _tokens_per_launch(hidden: int, inter: int, top_k: int, n_live: int) -> int:
+    """The most tokens one launch of the grouped kernels may take. They address activation
+    rows (x: hidden bf16 values per token) and intermediate rows (h: inter values per table
+    row) with 32-bit byte offsets, and the library refuses a launch whose tables could hold
+    rows past `_OFFSET_LIMIT`: at most n_blocks * 16 rows, i.e. the call's tokens * top_k
+    plus up to 15 padding rows per routed expert."""
+    rows = min(_OFFSET_LIMIT // (2 * inter), (_OFFSET_LIMIT // (2 * hidden)) * top_k)
+    return max((rows - (_PF_BLOCK_M - 1) * n_live) // top_k, 1)
+
+
+def _prefill_call(x, eidx_cpu, routing_weights, blobs, out, plan) -> None:
+    """The three kernels over one launch's tokens."""
     blob = blobs[int(plan[1][0])]
-    geom, sc = blob["geom"], _SCALE_CODE[blob["flat"]["scale"].dtype]
-    top_k = eidx_cpu.shape[1]
+    geom, sc, top_k = blob["geom"], _scale_code(blob), eidx_cpu.shape[1]
     x = x.contiguous()
     tbl, rows, order, n_blocks = _prefill_tables(eidx_cpu, plan, blobs, x.device)
     h = _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc)
     y = _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc)
-    if out.is_contiguous():
-        _reduce(y, order, out, top_k)
-    else:
-        dense = torch.empty(out.shape, dtype=torch.float32, device=out.device)
-        _reduce(y, order, dense, top_k)
+    dense = out if out.is_contiguous() else torch.empty(out.shape, dtype=torch.float32,
+                                                        device=out.device)
+    _reduce(y, order, dense, top_k)
+    if dense is not out:
         out.copy_(dense)
+
+
+def _prefill_launch(x, eidx_cpu, routing_weights, blobs, out, plan=None) -> None:
+    """The three prefill kernels over one call, unchecked (`_prefill_checked` gates this;
+    vaayu/packed_expert_kernels.py:760-777). A strided `x` is made dense; a strided `out` is
+    written through a dense temporary. A call too large for the kernels' 32-bit row offsets
+    is launched in token chunks, with the same bits (each row's arithmetic is its own)."""
+    plan = plan or _prefill_plan(eidx_cpu)
+    lay = _layout(blobs[int(plan[1][0])]["geom"])
+    top_k = eidx_cpu.shape[1]
+    step = _tokens_per_launch(lay["gate"][3], lay["gate"][2], top_k, plan[1].numel())
+    tokens = x.shape[0]
+    if tokens <= step:
+        _prefill_call(x, eidx_cpu, routing_weights, blobs, out, plan)
+        return
+    for t0 in range(0, tokens, step):
+        part = slice(t0, min(t0 + step, tokens))
+        e_part = eidx_cpu[part]
+        _prefill_call(x[part], e_part, routing_weights[part], blobs, out[part],
+                      _prefill_plan(e_part))
 
 
 def _linear_fp32(a, w):
@@ -630,10 +766,10 @@ def _linear_fp32(a, w):
 
 def stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn,
                           linear=F.linear) -> None:
-    """The per-slot loop's arithmetic for a multi-token call, into `out`
-    (vaayu/packed_expert_kernels.py:785-814): per expert in id order, gather its rows,
-    dense weights, three `linear`s, `act_fn`, the routing-weight product, `index_add_`.
-    A routed expert with no entry is skipped. `linear=_linear_fp32` is the reference the
+    """A multi-token call through the per-slot loop's arithmetic, into `out`
+    (vaayu/packed_expert_kernels.py:785-814): per expert in id order, its rows gathered,
+    dense weights, three `linear`s, `act_fn`, the routing-weight product, `index_add_`. A
+    routed expert with no entry is skipped. `linear=_linear_fp32` is the reference the
     kernels are checked against."""
     from .moe_patch import expert_weights_from_entry
     order, live, counts = _prefill_plan(eidx_cpu)
@@ -641,41 +777,36 @@ def stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn,
     rw = routing_weights.reshape(-1)
     order = order.to(x.device)
     out.zero_()
-    at = 0
-    for e, c in zip(live.tolist(), counts.tolist()):
-        rows = order[at:at + c]
-        at += c
+    for e, rows in zip(live.tolist(), torch.split(order, counts.tolist())):
         entry = blobs.get(e)
         if entry is None:
             continue
-        w_gate, w_down, w_up = expert_weights_from_entry(entry, x.dtype)
-        tok = rows // top_k
-        xs = x[tok]
-        y = linear(act_fn(linear(xs, w_gate)) * linear(xs, w_up), w_down)
-        out.index_add_(0, tok, (y * rw[rows, None]).to(out.dtype))
+        gate_w, down_w, up_w = expert_weights_from_entry(entry, x.dtype)
+        tokens = rows // top_k
+        xs = x[tokens]
+        hidden = act_fn(linear(xs, gate_w)) * linear(xs, up_w)
+        out.index_add_(0, tokens, (linear(hidden, down_w) * rw[rows, None]).to(out.dtype))
 
 
 def _prefill_verdict(x, eidx_cpu, routing_weights, blobs, act_fn, plan) -> bool:
-    """Run the grouped kernels AND the fp32-GEMM stock arithmetic on this call's data
+    """The grouped kernels AND the fp32-GEMM stock arithmetic on this call's data
     (vaayu/packed_expert_kernels.py:817-826)."""
     blob = blobs[int(plan[1][0])]
-    why = _prefill_unsupported(blob["geom"], x.dtype, blob["flat"]["scale"].dtype,
-                               routing_weights.dtype)
-    return _agrees(
-        why, x,
-        lambda ref: stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, ref, act_fn,
-                                          linear=_linear_fp32),
-        lambda got: _prefill_launch(x, eidx_cpu, routing_weights, blobs, got, plan), "prefill")
+    return _judge("prefill", x,
+                  _prefill_unsupported(blob["geom"], x.dtype, blob["flat"]["scale"].dtype,
+                                       routing_weights.dtype),
+                  lambda want: stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, want,
+                                                     act_fn, linear=_linear_fp32),
+                  lambda got: _prefill_launch(x, eidx_cpu, routing_weights, blobs, got, plan))
 
 
 def _prefill_checked(x, eidx_cpu, routing_weights, blobs, act_fn, plan) -> bool:
-    """The cached verdict for this call's (geometry, dtypes) key
-    (vaayu/packed_expert_kernels.py:829-835)."""
-    blob = blobs[int(plan[1][0])]
-    key = (blob["geom"], x.dtype, routing_weights.dtype, blob["flat"]["scale"].dtype)
-    if key not in _PF_VERDICTS:
-        _PF_VERDICTS[key] = _prefill_verdict(x, eidx_cpu, routing_weights, blobs, act_fn, plan)
-    return _PF_VERDICTS[key]
+    """The verdict of this call's (geometry, dtypes) key (vaayu/packed_expert_kernels.py:
+    829-835)."""
+    return _remembered("_PF_VERDICTS",
+                       _verdict_key(blobs[int(plan[1][0])], x, routing_weights),
+                       lambda: _prefill_verdict(x, eidx_cpu, routing_weights, blobs, act_fn,
+                                                plan))
 
 
 def packed_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn) -> None:
@@ -689,11 +820,11 @@ def packed_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn) -> 
                     routed expert sends the whole call to the stock arithmetic
     out             [tokens, hidden] float32, overwritten (a strided view is fine)"""
     plan = _prefill_plan(eidx_cpu)
-    geoms = {blobs[e].get("geom") if e in blobs else None for e in plan[1].tolist()}
-    if (len(geoms) != 1 or None in geoms
-            or not _aligned(blobs[e] for e in plan[1].tolist())):
-        stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn)
-    elif _prefill_checked(x, eidx_cpu, routing_weights, blobs, act_fn, plan):
+    routed = plan[1].tolist()
+    on_kernels = (all(e in blobs for e in routed)
+                  and _kernel_ready(blobs[e] for e in routed)
+                  and _prefill_checked(x, eidx_cpu, routing_weights, blobs, act_fn, plan))
+    if on_kernels:
         _prefill_launch(x, eidx_cpu, routing_weights, blobs, out, plan)
     else:
         stock_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn)
@@ -702,12 +833,13 @@ def packed_experts_prefill(x, eidx_cpu, routing_weights, blobs, out, act_fn) -> 
 # ── load-time install ─────────────────────────────────────────────────────────────────────
 
 def _is_silu(act_fn, device, dtype) -> bool:
-    """Behavioural: does the experts' activation compute SiLU? (the kernels hardcode it)"""
+    """Does the experts' activation compute SiLU (which the kernels hardcode)? Judged by
+    its values on a grid, since the module may be any callable."""
     if act_fn is None:
         return False
-    t = torch.linspace(-8.0, 8.0, 257, device=device).to(dtype)
+    probe = torch.linspace(-8.0, 8.0, 257, device=device).to(dtype)
     try:
-        return torch.equal(act_fn(t), F.silu(t))
+        return torch.equal(act_fn(probe), F.silu(probe))
     except Exception:
         return False
 
@@ -717,38 +849,37 @@ _ST_DTYPES = {"BF16": torch.bfloat16, "F16": torch.float16, "F32": torch.float32
 
 
 def _read_expert_tensors(path: str, metas: dict) -> dict:
-    """{key: cpu tensor} for one expert's tensors of a safetensors shard, read at the byte
+    """{key: cpu tensor} of one expert's tensors in a safetensors shard, read at the byte
     ranges the engine's offset index records (file_offset, byte_length, shape, dtype)."""
     out = {}
     with open(path, "rb") as f:
         for key, m in metas.items():
             f.seek(m.file_offset)
-            buf = bytearray(f.read(m.byte_length))
-            t = torch.frombuffer(buf, dtype=_ST_DTYPES[m.dtype]) if buf else torch.empty(0)
-            out[key] = t.reshape(m.shape).clone()
+            raw = bytearray(f.read(m.byte_length))
+            flat = torch.frombuffer(raw, dtype=_ST_DTYPES[m.dtype]) if raw else torch.empty(0)
+            out[key] = flat.reshape(m.shape).clone()
     return out
 
 
 def _one_real_blob(vaayu_ref, block, device, quiet=False):
-    """The blob of `block`'s lowest-numbered expert read off the checkpoint, or None when
+    """The blob of `block`'s lowest-numbered expert as the checkpoint stores it, or None when
     its experts are not pack-quantized (vaayu/packed_expert_kernels.py:875-899)."""
     from .moe_patch import (_group_packed_tensors_by_weight, _packed_roles_complete,
                             _upload_packed_expert, build_expert_blob)
     metas = vaayu_ref._expert_offset_index.index.get(block.layer_name, {})
     if not metas:
         return None
-    path = str(Path(vaayu_ref.checkpoint_path) / f"{block.layer_name}.safetensors")
+    shard = Path(vaayu_ref.checkpoint_path) / f"{block.layer_name}.safetensors"
     try:     # inside the engine, its own reader (io_uring, pinned buffers)
-        from vaayu.persist.safetensor_model_persister import load_expert_sparse
+        from vaayu.persist.safetensor_model_persister import load_expert_sparse as read
     except ImportError:
-        load_expert_sparse = _read_expert_tensors
-    raw = load_expert_sparse(path, metas[min(metas)])
-    packed = _group_packed_tensors_by_weight(raw)
-    if not packed["gate"] or not _packed_roles_complete(packed):
+        read = _read_expert_tensors
+    roles = _group_packed_tensors_by_weight(read(str(shard), metas[min(metas)]))
+    if not roles["gate"] or not _packed_roles_complete(roles):
         return None
-    why = "its projections are packed at different bit widths or group sizes"
     try:
-        blob = build_expert_blob(_upload_packed_expert(packed, device))
+        blob = build_expert_blob(_upload_packed_expert(roles, device))
+        why = "its projections are packed at different bit widths or group sizes"
     except NotImplementedError as exc:
         blob, why = None, str(exc)
     if blob is None and not quiet:
@@ -759,60 +890,56 @@ def _one_real_blob(vaayu_ref, block, device, quiet=False):
 _PREFILL_VRAM_HEADROOM = 4 << 30
 
 
-def install_packed_expert_kernels(vaayu_ref) -> bool:
-    """Route the fused pack-quantized MoE blocks through the kernels if they agree with
-    the stock arithmetic on one real expert of this model on this device
-    (vaayu/packed_expert_kernels.py:902-1012). Sets `vaayu_ref._packed_moe_kernel` (decode)
-    and `vaayu_ref._packed_moe_prefill_kernel` (the eligible prefill layers); returns
-    whether the decode kernel was installed."""
+def _describe(geom) -> str:
+    """"4-bit, group 128" for integer blobs (the reference's wording); the format and its
+    scale blocking for FP8 / MXFP4 blobs."""
+    if isinstance(geom[0], str):
+        return f"{geom[0]}, scale block {geom[1]}"
+    return f"{geom[0]}-bit, group {geom[1]}"
+
+
+def _install_preconditions(vaayu_ref):
+    """(device, dtype, fused blocks) when the kernels could be installed, else None (with
+    the WARNING the reference prints for a missing library or a non-current device)."""
     device = str(vaayu_ref.running_device)
     if torch.device(device).type != "cuda":
-        return False
+        return None
     if triton is None:
         if torch.cuda.is_available():
             print(f"[Vaayu] WARNING: fused packed-expert kernels not installed: "
-                  f"{globals().get('_LOAD_ERROR', 'the kernel library is absent')}")
-        return False
+                  f"{_LOAD_ERROR or 'the kernel library is absent'}")
+        return None
     blocks = [b for b in (getattr(vaayu_ref, "_moe_blocks", None) or [])
               if getattr(b, "forward_name", None) == "_make_fused_sparse_forward"]
     if not blocks or getattr(vaayu_ref, "_expert_offset_index", None) is None:
-        return False
-    dev_index = torch.device(device).index
-    if dev_index is not None and dev_index != torch.cuda.current_device():
+        return None
+    index = torch.device(device).index
+    if index is not None and index != torch.cuda.current_device():
         print(f"[Vaayu] WARNING: fused packed-expert decode kernel not installed: model "
               f"device {device} is not the current GPU ({torch.cuda.current_device()}); "
               f"decode keeps the stock per-expert path")
-        return False
-    block, dtype = blocks[0], vaayu_ref.running_dtype
-    act_fn = getattr(getattr(block.moe_module, block.experts_attr, None), "act_fn", None)
-    if not _is_silu(act_fn, device, dtype):
-        print("[Vaayu] fused packed-expert decode kernel not used: the experts' activation "
-              "is not SiLU")
-        return False
-    blob = _one_real_blob(vaayu_ref, block, device)
-    if blob is None:
-        return False
-    k = int(getattr(vaayu_ref, "moe_top_k", 0) or 1)
-    gen = torch.Generator(device=device).manual_seed(0)
-    x = (torch.randn(1, _layout(blob["geom"])["gate"][3], generator=gen, device=device)
-         * 0.5).to(dtype)
-    w = torch.rand(1, k, generator=gen, device=device) + 0.1
-    w = w / w.sum(-1, keepdim=True)
-    pairs = [(blob, s) for s in range(k)]
-    if not all(_checked(x, pairs, rw, act_fn) for rw in (w, w.to(dtype))):
-        return False
-    vaayu_ref._packed_moe_kernel = blob["geom"]
-    bits, gs, _roles = blob["geom"]
-    print(f"[Vaayu] fused packed-expert decode kernel on {len(blocks)} MoE layers "
-          f"({bits}-bit, group {gs})")
-    try:
-        from vaayu.moe_patch import _PREFILL_VRAM_HEADROOM as headroom
-    except ImportError:
-        headroom = _PREFILL_VRAM_HEADROOM
+        return None
+    return device, vaayu_ref.running_dtype, blocks
+
+
+def _probe_inputs(blob, tokens, top_k, device, dtype, gen):
+    """Seeded activations [tokens, hidden] and routing weights [tokens, top_k] (rows sum to
+    one; fp32) for the load-time verdicts."""
+    hidden = _layout(blob["geom"])["gate"][3]
+    x = (torch.randn(tokens, hidden, generator=gen, device=device) * 0.5).to(dtype)
+    w = torch.rand(tokens, top_k, generator=gen, device=device) + 0.1
+    return x, w / w.sum(-1, keepdim=True)
+
+
+def _prefill_eligibility(vaayu_ref, blocks, first, blob, device, headroom):
+    """(eligible layer indices, {reason: [layer indices]}) over the fused blocks: a layer
+    qualifies when one real expert of it has the checked layer's geometry and scale dtype
+    and its whole expert set fits in half the prefill headroom (a call holds every blob it
+    uploaded until its launches run)."""
     checked = (blob["geom"], blob["flat"]["scale"].dtype)
-    eligible, skipped = [], {}
+    eligible, left_out = [], {}
     for b in blocks:
-        one = blob if b is block else _one_real_blob(vaayu_ref, b, device, quiet=True)
+        one = blob if b is first else _one_real_blob(vaayu_ref, b, device, quiet=True)
         if one is None:
             why = "experts not pack-quantized, or packed with no fused pass"
         elif (one["geom"], one["flat"]["scale"].dtype) != checked:
@@ -826,29 +953,77 @@ def install_packed_expert_kernels(vaayu_ref) -> bool:
             why = (f"one call can hold a layer's {n_experts} experts on the GPU at once "
                    f"({held / 2**30:.2f} GiB), over half the "
                    f"{headroom / 2**30:.2f} GiB prefill headroom")
-        skipped.setdefault(why, []).append(b.layer_idx)
+        left_out.setdefault(why, []).append(b.layer_idx)
+    return eligible, left_out
+
+
+def _prefill_holds(blob, top_k, device, dtype, act_fn, gen) -> bool:
+    """The prefill verdict on a call of 1.5 blocks of tokens, every token routed to every
+    slot of the one real expert (in rotating slot order), with fp32 and activation-dtype
+    routing weights."""
+    tokens = _PF_BLOCK_M + _PF_BLOCK_M // 2
+    eidx = torch.stack([torch.roll(torch.arange(top_k), t) for t in range(tokens)])
+    xs, ws = _probe_inputs(blob, tokens, top_k, device, dtype, gen)
+    blobs = dict.fromkeys(range(top_k), blob)
+    plan = _prefill_plan(eidx)
+    return all(_prefill_checked(xs, eidx, w, blobs, act_fn, plan) for w in (ws, ws.to(dtype)))
+
+
+def _announce_prefill(eligible, left_out, n_blocks, what) -> None:
+    print(f"[Vaayu] fused packed-expert prefill kernel on {len(eligible)} MoE layers ({what})")
+    if not left_out:
+        return
+    skipped = sorted(i for idxs in left_out.values() for i in idxs)
+    reasons = "; ".join(
+        why if len(left_out) == 1 else f"{why} (layers {', '.join(map(str, idxs))})"
+        for why, idxs in left_out.items())
+    print(f"[Vaayu] WARNING: fused packed-expert prefill kernel not used on {len(skipped)} of "
+          f"{n_blocks} MoE layers (layer indices {', '.join(map(str, skipped))}): {reasons}; "
+          f"prefill keeps the per-expert path there")
+
+
+def install_packed_expert_kernels(vaayu_ref) -> bool:
+    """Route the fused pack-quantized MoE blocks through the kernels if they agree with the
+    stock arithmetic on one real expert of this model on this device
+    (vaayu/packed_expert_kernels.py:902-1012). Sets `vaayu_ref._packed_moe_kernel` (decode)
+    and `vaayu_ref._packed_moe_prefill_kernel` (the eligible prefill layers); returns
+    whether the decode kernel was installed."""
+    ready = _install_preconditions(vaayu_ref)
+    if ready is None:
+        return False
+    device, dtype, blocks = ready
+    first = blocks[0]
+    act_fn = getattr(getattr(first.moe_module, first.experts_attr, None), "act_fn", None)
+    if not _is_silu(act_fn, device, dtype):
+        print("[Vaayu] fused packed-expert decode kernel not used: the experts' activation "
+              "is not SiLU")
+        return False
+    blob = _one_real_blob(vaayu_ref, first, device)
+    if blob is None:
+        return False
+
+    # decode: one token over every slot of the real expert, fp32 and activation-dtype weights
+    top_k = int(getattr(vaayu_ref, "moe_top_k", 0) or 1)
+    gen = torch.Generator(device=device).manual_seed(0)
+    x, w = _probe_inputs(blob, 1, top_k, device, dtype, gen)
+    pairs = [(blob, s) for s in range(top_k)]
+    if not all(_checked(x, pairs, rw, act_fn) for rw in (w, w.to(dtype))):
+        return False
+    vaayu_ref._packed_moe_kernel = blob["geom"]
+    what = _describe(blob["geom"])
+    print(f"[Vaayu] fused packed-expert decode kernel on {len(blocks)} MoE layers ({what})")
+
+    # prefill: the layers that qualify, then the verdict on one real call
+    try:
+        from vaayu.moe_patch import _PREFILL_VRAM_HEADROOM as headroom
+    except ImportError:
+        headroom = _PREFILL_VRAM_HEADROOM
+    eligible, left_out = _prefill_eligibility(vaayu_ref, blocks, first, blob, device, headroom)
     if not eligible:
         print(f"[Vaayu] WARNING: fused packed-expert prefill kernel not installed: "
-              f"{'; '.join(skipped)}; prefill keeps the per-expert path")
+              f"{'; '.join(left_out)}; prefill keeps the per-expert path")
         return True
-    tokens = _PF_BLOCK_M + _PF_BLOCK_M // 2
-    eidx = torch.stack([torch.roll(torch.arange(k), t) for t in range(tokens)])
-    xs = (torch.randn(tokens, x.shape[1], generator=gen, device=device) * 0.5).to(dtype)
-    ws = torch.rand(tokens, k, generator=gen, device=device) + 0.1
-    ws = ws / ws.sum(-1, keepdim=True)
-    blobs = {e: blob for e in range(k)}
-    plan = _prefill_plan(eidx)
-    if all(_prefill_checked(xs, eidx, rw, blobs, act_fn, plan) for rw in (ws, ws.to(dtype))):
+    if _prefill_holds(blob, top_k, device, dtype, act_fn, gen):
         vaayu_ref._packed_moe_prefill_kernel = frozenset(eligible)
-        print(f"[Vaayu] fused packed-expert prefill kernel on {len(eligible)} MoE layers "
-              f"({bits}-bit, group {gs})")
-        if skipped:
-            left_out = sorted(i for idxs in skipped.values() for i in idxs)
-            whys = "; ".join(
-                why if len(skipped) == 1 else f"{why} (layers {', '.join(map(str, idxs))})"
-                for why, idxs in skipped.items())
-            print(f"[Vaayu] WARNING: fused packed-expert prefill kernel not used on "
-                  f"{len(left_out)} of {len(blocks)} MoE layers (layer indices "
-                  f"{', '.join(map(str, left_out))}): {whys}; prefill keeps the per-expert "
-                  f"path there")
+        _announce_prefill(eligible, left_out, len(blocks), what)
     return True
