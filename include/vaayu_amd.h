@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 6
+#define VAAYU_ABI_VERSION 7
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -243,6 +243,20 @@ int vaayu_fused3d_down(const void *h, const int64_t *rows, const int64_t *tbl,
                        const int64_t *btbl, const float *gammas, float *y, int32_t n_blocks,
                        int32_t top_k, int32_t hidden, int32_t inter, int32_t inter_pad,
                        const void *codes_end, const void *scales_end, void *stream);
+
+/* One-token decode that allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and result as
+ * vaayu_decode_gate_up followed by vaayu_decode_down, without `h`: the intermediate
+ * [n_pairs, inter] lives in a file-scope device array of
+ * vaayu_decode_noalloc_scratch_bytes() bytes (4 MiB) held by each GPU until the process
+ * ends. Returns -3 when n_pairs * inter * sizeof(act) exceeds it. Calls that overlap on
+ * one GPU (other streams or threads) share the array and race. The first call on a device
+ * looks the array's address up (hipGetSymbolAddress); make it outside a graph capture. */
+int vaayu_decode_noalloc(const void *x, const int64_t *table, const void *routing_weights,
+                         int32_t rw_dtype, float *out, int32_t n_pairs, const vaayu_geom *geom,
+                         int32_t act, int32_t scale_dtype, int32_t w_round, void *stream);
+int64_t vaayu_decode_noalloc_scratch_bytes(void);
 
 #ifdef __cplusplus
 }
