@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 7
+#define VAAYU_ABI_VERSION 8
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -257,6 +257,30 @@ int vaayu_decode_noalloc(const void *x, const int64_t *table, const void *routin
                          int32_t rw_dtype, float *out, int32_t n_pairs, const vaayu_geom *geom,
                          int32_t act, int32_t scale_dtype, int32_t w_round, void *stream);
 int64_t vaayu_decode_noalloc_scratch_bytes(void);
+
+/* Decode, both stages in ONE launch. Replaces the `_gate_up` + `_down` pair
+ * (vaayu/packed_expert_kernels.py:355-387) that `_launch` / the per-layer graph run
+ * (:390-396, 578-654): same arguments and result as vaayu_decode_gate_up followed by
+ * vaayu_decode_down (h [n_pairs, inter] is the caller's buffer), bf16 / fp16 activations and
+ * 4- / 8-bit codes only. The down workgroups request their codes while the gate/up
+ * workgroups run and wait on per-workgroup counters in `sync` (int32
+ * [vaayu_decode_fused_sync_words(...)], zeroed before its first call): one sync buffer
+ * per launch configuration (geometry, n_pairs, dtypes), used by one stream at a time.
+ * max_polls bounds a down workgroup's wait (0: about a second); past it the last word of
+ * sync is set nonzero and the output is undefined. */
+int vaayu_decode_fused(const void *x, const int64_t *table, const void *routing_weights,
+                       int32_t rw_dtype, float *out, void *h, int32_t *sync, int32_t n_pairs,
+                       const vaayu_geom *geom, int32_t act, int32_t scale_dtype,
+                       int32_t w_round, int32_t max_polls, void *stream);
+/* Words of vaayu_decode_fused's sync buffer for this configuration, or a negative code. */
+int32_t vaayu_decode_fused_sync_words(int32_t n_pairs, const vaayu_geom *geom, int32_t act,
+                                      int32_t scale_dtype);
+
+/* Measurement only (no counterpart in the reference): `blocks` workgroups of 4 waves each
+ * issue `iters` rounds of 16 independent v_mfma_f32_16x16x32_bf16 from registers; out
+ * [blocks * 256] fp32 receives one sum per lane. 2 * 16 * 16 * 32 * 16 * iters * 4 * blocks
+ * FLOPs per launch: the benchmark's measured bf16 matrix-core peak. */
+int vaayu_probe_mfma(float *out, int32_t blocks, int32_t iters, void *stream);
 
 #ifdef __cplusplus
 }

@@ -4,13 +4,6 @@
 
 namespace vaayu {
 
-struct DownPlan {
-  MShape s;
-  int kp, ps, nrg;
-  size_t lds;
-  unsigned blocks;
-};
-
 // Step counts with a straight-line kernel; others run the chunked loop (NS = 0).
 template <int F, int ACT, int SW>
 static int mfma_down_at(const void* h, const int64_t* tbl, const void* rw, int rw_dt, float* out,
@@ -46,44 +39,6 @@ static int mfma_down_sw(const void* h, const int64_t* tbl, const void* rw, int r
     if (sc == DT_FP32) return mfma_down_at<F, ACT, 32>(h, tbl, rw, rw_dt, out, d, w_round, st);
     return mfma_down_at<F, ACT, 16>(h, tbl, rw, rw_dt, out, d, w_round, st);
   }
-}
-
-// The MFMA kernel's plan for this launch, or false when it does not take it. K parts: the
-// most of 4, 2, 1 that split the intermediate dimension into whole steps (4 units each).
-// Row groups per wave (nrg) keep the grid at kMaxDownBlocks blocks at most, since every
-// block stages all pairs' h. A wave starts a row group's requests only when the previous
-// one is done, so each extra row group exposes a full memory latency; up to 2048 blocks
-// (h re-read from L2 per block) the straight one-group kernel is the faster trade.
-constexpr int64_t kMaxDownBlocks = 2048;
-
-static bool mfma_down_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, DownPlan& d) {
-  if (!mfma_format(fmt, act)) return false;
-  const int cpu = 128 / (fmt % 100);
-  if (g->inter % cpu) return false;
-  const int units = g->inter / cpu;
-  d.kp = units % 16 == 0 ? 4 : units % 8 == 0 ? 2 : units % 4 == 0 ? 1 : 0;
-  if (!d.kp) return false;
-  d.s = mfma_shape(g, fmt, n, g->hidden, g->inter, d.kp, sc);
-  const int64_t vec16 = (int64_t)n * g->inter / 8;
-  if (vec16 > 8 * 512) return false;                          // h: up to 8 uint4 per thread
-  d.s.vec16 = (int)vec16;
-  d.ps = 1;
-  while (d.ps < 8 && d.ps < n) d.ps <<= 1;
-  const int rows_g = (8 / d.ps) * (16 / d.kp);               // rows per block per row group
-  const int64_t blocks1 = (g->hidden + rows_g - 1) / rows_g;
-  d.nrg = (int)std::max<int64_t>(1, (blocks1 + kMaxDownBlocks - 1) / kMaxDownBlocks);
-  const int br = d.nrg * rows_g;
-  d.blocks = (unsigned)((g->hidden + br - 1) / br);
-  d.lds = (size_t)vec16 * 16 + (size_t)n * br * sizeof(float);
-  if (d.lds > 64 * 1024) return false;
-  const int64_t role_bytes = (int64_t)g->hidden * g->inter * g->bits / 8;
-  const int64_t role_scales = (int64_t)(g->hidden >> d.s.rshift) * (g->inter / g->group);
-  if (role_bytes > 0xFFFFFFFFll || role_scales * scale_bytes_of(sc) > 0xFFFFFFFFll) return false;
-  d.s.wb0 = (uint32_t)(g->down_w * 4);
-  d.s.sc0 = (uint32_t)g->down_s;
-  d.s.code_bytes = (uint32_t)role_bytes;
-  d.s.scale_bytes = (uint32_t)(role_scales * scale_bytes_of(sc));
-  return true;
 }
 
 template <int BITS, int ACT, int SW, int CH>

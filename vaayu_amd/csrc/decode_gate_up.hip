@@ -52,32 +52,6 @@ static int mfma_gate_up_sw(const void* x, const int64_t* tbl, void* h, const MSh
   }
 }
 
-// The MFMA kernel's shape for this launch, or false when it does not take it: hidden is a
-// multiple of 16 units (4 K parts x 4 lane quarters), x fits 4 uint4 per thread, and the
-// two roles lie within 4 GiB of the blob's packed address.
-static bool mfma_gate_up_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, MShape& s,
-                              int& xs) {
-  if (!mfma_format(fmt, act)) return false;
-  const int cpu = 128 / (fmt % 100);
-  if (g->hidden % cpu || (g->hidden / cpu) % 16) return false;
-  s = mfma_shape(g, fmt, n, g->inter, g->hidden, 4, sc);
-  s.vec16 = g->hidden / 8;
-  xs = (s.vec16 + 255) / 256;
-  if (xs > 4) return false;
-  const int64_t role_bytes = (int64_t)g->inter * g->hidden * g->bits / 8;
-  const int64_t code_end = std::max(g->gate_w, g->up_w) * 4 + role_bytes;
-  const int64_t role_scales = (int64_t)(g->inter >> s.rshift) * (g->hidden / g->group);
-  const int64_t scale_end = (std::max(g->gate_s, g->up_s) + role_scales) * scale_bytes_of(sc);
-  if (code_end > 0xFFFFFFFFll || scale_end > 0xFFFFFFFFll) return false;
-  s.wb0 = (uint32_t)(g->gate_w * 4);
-  s.wb1 = (uint32_t)(g->up_w * 4);
-  s.sc0 = (uint32_t)g->gate_s;
-  s.sc1 = (uint32_t)g->up_s;
-  s.code_bytes = (uint32_t)code_end;
-  s.scale_bytes = (uint32_t)scale_end;
-  return true;
-}
-
 // Fast path: 4/8-bit codes with bf16/fp16 activations, any CH of the instantiated set.
 // General path (fp32 activations, 1/2-bit codes): CH = 1.
 template <int BITS, int ACT, int SW, int CH>

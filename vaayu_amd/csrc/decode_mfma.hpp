@@ -14,6 +14,8 @@
 // Rows m >= KP of A are left as whatever the lanes hold: D rows other than D[kp(c)][c] are
 // never read.
 #pragma once
+#include <algorithm>
+
 #include "decode_kernels.hpp"
 
 namespace vaayu {
@@ -341,5 +343,77 @@ inline MShape mfma_shape(const vaayu_geom* g, int fmt, int n, int rows, int k_di
 
 // Bytes of a scale of dtype code `sc` (E8M0: 1).
 inline int scale_bytes_of(int sc) { return sc == DT_FP32 ? 4 : sc == VAAYU_E8M0 ? 1 : 2; }
+
+// The MFMA kernel's shape for this launch, or false when it does not take it: hidden is a
+// multiple of 16 units (4 K parts x 4 lane quarters), x fits 4 uint4 per thread, and the
+// two roles lie within 4 GiB of the blob's packed address.
+inline bool mfma_gate_up_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, MShape& s,
+                              int& xs) {
+  if (!mfma_format(fmt, act)) return false;
+  const int cpu = 128 / (fmt % 100);
+  if (g->hidden % cpu || (g->hidden / cpu) % 16) return false;
+  s = mfma_shape(g, fmt, n, g->inter, g->hidden, 4, sc);
+  s.vec16 = g->hidden / 8;
+  xs = (s.vec16 + 255) / 256;
+  if (xs > 4) return false;
+  const int64_t role_bytes = (int64_t)g->inter * g->hidden * g->bits / 8;
+  const int64_t code_end = std::max(g->gate_w, g->up_w) * 4 + role_bytes;
+  const int64_t role_scales = (int64_t)(g->inter >> s.rshift) * (g->hidden / g->group);
+  const int64_t scale_end = (std::max(g->gate_s, g->up_s) + role_scales) * scale_bytes_of(sc);
+  if (code_end > 0xFFFFFFFFll || scale_end > 0xFFFFFFFFll) return false;
+  s.wb0 = (uint32_t)(g->gate_w * 4);
+  s.wb1 = (uint32_t)(g->up_w * 4);
+  s.sc0 = (uint32_t)g->gate_s;
+  s.sc1 = (uint32_t)g->up_s;
+  s.code_bytes = (uint32_t)code_end;
+  s.scale_bytes = (uint32_t)scale_end;
+  return true;
+}
+
+struct DownPlan {
+  MShape s;
+  int kp, ps, nrg;
+  size_t lds;
+  unsigned blocks;
+};
+
+// The MFMA kernel's plan for this launch, or false when it does not take it. K parts: the
+// most of 4, 2, 1 that split the intermediate dimension into whole steps (4 units each).
+// Row groups per wave (nrg) keep the grid at kMaxDownBlocks blocks at most, since every
+// block stages all pairs' h. A wave starts a row group's requests only when the previous
+// one is done, so each extra row group exposes a full memory latency; up to 2048 blocks
+// (h re-read from L2 per block) the straight one-group kernel is the faster trade.
+constexpr int64_t kMaxDownBlocks = 2048;
+
+inline bool mfma_down_plan(const vaayu_geom* g, int fmt, int act, int n, int sc, DownPlan& d) {
+  if (!mfma_format(fmt, act)) return false;
+  const int cpu = 128 / (fmt % 100);
+  if (g->inter % cpu) return false;
+  const int units = g->inter / cpu;
+  d.kp = units % 16 == 0 ? 4 : units % 8 == 0 ? 2 : units % 4 == 0 ? 1 : 0;
+  if (!d.kp) return false;
+  d.s = mfma_shape(g, fmt, n, g->hidden, g->inter, d.kp, sc);
+  const int64_t vec16 = (int64_t)n * g->inter / 8;
+  if (vec16 > 8 * 512) return false;                          // h: up to 8 uint4 per thread
+  d.s.vec16 = (int)vec16;
+  d.ps = 1;
+  while (d.ps < 8 && d.ps < n) d.ps <<= 1;
+  const int rows_g = (8 / d.ps) * (16 / d.kp);               // rows per block per row group
+  const int64_t blocks1 = (g->hidden + rows_g - 1) / rows_g;
+  d.nrg = (int)std::max<int64_t>(1, (blocks1 + kMaxDownBlocks - 1) / kMaxDownBlocks);
+  const int br = d.nrg * rows_g;
+  d.blocks = (unsigned)((g->hidden + br - 1) / br);
+  d.lds = (size_t)vec16 * 16 + (size_t)n * br * sizeof(float);
+  if (d.lds > 64 * 1024) return false;
+  const int64_t role_bytes = (int64_t)g->hidden * g->inter * g->bits / 8;
+  const int64_t role_scales = (int64_t)(g->hidden >> d.s.rshift) * (g->inter / g->group);
+  if (role_bytes > 0xFFFFFFFFll || role_scales * scale_bytes_of(sc) > 0xFFFFFFFFll) return false;
+  d.s.wb0 = (uint32_t)(g->down_w * 4);
+  d.s.sc0 = (uint32_t)g->down_s;
+  d.s.code_bytes = (uint32_t)role_bytes;
+  d.s.scale_bytes = (uint32_t)(role_scales * scale_bytes_of(sc));
+  return true;
+}
+
 
 }  // namespace vaayu

@@ -394,6 +394,30 @@ def _launch(x, pairs, routing_weights, out) -> None:
     _down(h, tbl, routing_weights, out, len(pairs), blob["geom"], _scale_code(blob))
 
 
+def _fused_sync_words(n_pairs, geom, act_dtype, scale_dtype):
+    """int32 words of the one-launch decode's sync buffer for this configuration, or None
+    when the one-launch kernel does not take it."""
+    lib = _require_backend()
+    words = lib.vaayu_decode_fused_sync_words(n_pairs, _lib.geom_struct(geom),
+                                              _DTYPE_CODE[act_dtype], _SCALE_CODE[scale_dtype])
+    return words if words > 0 else None
+
+
+def _fused(x, tbl, n, geom, sc, routing_weights, out, h, sync, max_polls=0) -> None:
+    """Both decode stages in one launch (`vaayu_decode_fused`): the arithmetic of `_gate_up`
+    then `_down`, with the down workgroups streaming their codes while gate/up runs. `sync`
+    is the configuration's zero-initialised int32 counter buffer (`_fused_sync_words`)."""
+    lib = _require_backend()
+    rw = routing_weights.reshape(-1).contiguous()
+    _lib.check(lib.vaayu_decode_fused(x.data_ptr(), tbl.data_ptr(), rw.data_ptr(),
+                                      _DTYPE_CODE[rw.dtype], out.data_ptr(), h.data_ptr(),
+                                      sync.data_ptr(), n, _lib.geom_struct(geom),
+                                      _DTYPE_CODE[x.dtype], sc,
+                                      int(_rounds_weighted(rw.dtype, x.dtype)), max_polls,
+                                      _lib.stream_ptr(x.device)),
+               "vaayu_decode_fused")
+
+
 def stock_experts_decode(x, pairs, routing_weights, out, act_fn) -> None:
     """One token through the per-slot loop's arithmetic, into `out`: the reference the
     kernels are held to and their fallback (vaayu/packed_expert_kernels.py:399-410) --
