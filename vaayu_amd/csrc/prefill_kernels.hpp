@@ -42,11 +42,12 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 //
 // A work item is a RUN of up to R consecutive 16-row blocks of one expert (the table lists
 // each expert's blocks contiguously) times kTileN weight rows (N); R is kRunGateUp for gate/up,
-// whose two roles hold twice the accumulators, and kRunDown for down. Runs split where the
-// expert changes and at block indices that are multiples of R, so a block can tell from the
-// table alone whether it leads a run (its predecessor is another expert, or its index is a
-// multiple of R) and how long the run is; items of non-leading blocks exit at once. The
-// kernels branch once on the run's length S to a K loop compiled for that S.
+// whose two roles hold twice the accumulators, and kRunDown for down. An expert's blocks
+// form runs of R from its first block on (an expert of k blocks takes ceil(k / R) runs), so
+// a block can tell from the table alone whether it leads a run (its predecessor is another
+// expert, or it lies a multiple of R blocks past its expert's first block) and how long the
+// run is; items of non-leading blocks exit at once. The kernels branch once on the run's
+// length S to a K loop compiled for that S.
 //
 // Per K step (4 units of codes per weight row) the block stages the run's activation rows
 // in LDS, each wave dequantizes its 16 weight rows' codes ONCE in VGPRs straight into MFMA B
@@ -54,10 +55,9 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // shared by up to R*16 rows. The A operand of sub-tile s comes from LDS with the same K-slot
 // map as B (quarter q of the wave, MFMA i: codes [q*CPU + 8i, +8) of the step).
 //
-// XCD mapping: linear workgroup id L runs on XCD L % 8. Blocks are grouped by b / R (at most
-// one full run per group) and group G is placed on XCD G % 8, with all of a group's N tiles
-// consecutive in that XCD's order, so the items that share a run's activation rows share an
-// L2.
+// XCD mapping: linear workgroup id L runs on XCD L % 8. Blocks are grouped by b / R and group
+// G is placed on XCD G % 8, with all of a group's N tiles consecutive in that XCD's order, so
+// the items that share a run's activation rows (those of its leading block) share an L2.
 
 constexpr int kRunGateUp = 8;    // blocks per run, gate/up (two roles of accumulators)
 constexpr int kRunDown = 8;      // blocks per run, down
@@ -74,9 +74,20 @@ __device__ __forceinline__ RunInfo run_of(const int64_t* __restrict__ tbl, int b
   RunInfo r{0, 0};
   if (b >= n_blocks) return r;
   const int64_t me = tbl[2 * b];
-  if (b % R != 0 && tbl[2 * (b - 1)] == me) return r;
+  if (b > 0 && tbl[2 * (b - 1)] == me) {
+    // not its expert's first block: find the first (64 table entries a probe, one per
+    // lane), and lead only R, 2R, ... blocks on from it
+    const int lane = threadIdx.x & 63;
+    int first = -1;
+    for (int base = b - 1; first < 0; base -= 64) {
+      const int c = base - lane;
+      const uint64_t other = __ballot(c < 0 || tbl[2 * c] != me);
+      if (other) first = base - (__ffsll((unsigned long long)other) - 1) + 1;
+    }
+    if ((b - first) % R != 0) return r;
+  }
   int n = 1;
-  while (n < R && b + n < n_blocks && (b + n) % R != 0 && tbl[2 * (b + n)] == me) ++n;
+  while (n < R && b + n < n_blocks && tbl[2 * (b + n)] == me) ++n;
   r.lead = 1;
   r.nblk = n;
   return r;
