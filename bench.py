@@ -62,6 +62,7 @@ def parse():
 # WRITE_SIZE of a dispatch are scaled by (256 MiB / what the counter reads for that
 # calibration dispatch), which turns the counters into HBM bytes.
 CALIB_BYTES = 256 << 20
+WARM_MS = 150.0              # each graph's replays before it is timed, in ms of GPU work
 TRAFFIC_FILES = {"qwen3-decode": "decode_qwen3_b1_traffic.txt",
                  "mixtral-decode": "decode_mixtral_b1_traffic.txt",
                  "dsv3-decode": "decode_dsv3_b1_traffic.txt",
@@ -94,12 +95,14 @@ MARK_KERNEL = "bitwise_not"            # the marker launched around each timed r
 
 def _regions(d):
     """Per-kernel durations inside each timed region of a kernel trace: the dispatches
-    between consecutive marker dispatches (region k lies between marker k and k + 1)."""
+    between the marker dispatches that open and close it (the first marker is the one
+    launched when the markers are set up; region k lies between markers 2k + 1 and 2k + 2,
+    and the warm-up of the next region between 2k + 2 and 2k + 3)."""
     rows = _csv_rows(d, "kernel_trace.csv")
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    marks = [i for i, r in enumerate(rows) if MARK_KERNEL in r["Kernel_Name"]]
+    marks = [i for i, r in enumerate(rows) if MARK_KERNEL in r["Kernel_Name"]][1:]
     out = []
-    for k, (a, b) in enumerate(zip(marks, marks[1:])):
+    for k, (a, b) in enumerate(zip(marks[0::2], marks[1::2])):
         inside = rows[a + 1:b]
         if not inside:
             continue
@@ -162,13 +165,30 @@ def summarize(dirs):
             tag = next((k for k in TRAFFIC_KERNELS if k in name), None)
             if tag is not None:
                 out.append(f"traffic_bytes {tag} {ctr} {scaled:.0f}")
+        # bytes read from memory by L2 misses, counted by request size: exact for the
+        # calibration copy (no scale factor), unlike FETCH_SIZE on this chip
+        sizes = {"TCC_EA0_RDREQ_32B_sum": 32, "TCC_EA0_RDREQ_64B_sum": 64,
+                 "TCC_EA0_RDREQ_128B_sum": 128}
+        names = sorted({n for (n, c) in per if c in sizes})
+        if names:
+            out.append("")
+            out.append(f"{'kernel':<90} {'read bytes/dispatch (32/64/128-byte requests)':>46}")
+        for name in names:
+            if not all((name, c) in per for c in sizes):
+                continue
+            rb = sum(w * sum(per[(name, c)]) / len(per[(name, c)]) for c, w in sizes.items())
+            out.append(f"{name:<90} {rb:>46.0f}")
+            tag = next((k for k in TRAFFIC_KERNELS if k in name), None)
+            if tag is not None:
+                out.append(f"traffic_bytes {tag} READ_BYTES {rb:.0f}")
     return "\n".join(out)
 
 
 def traffic_from_profile(workload, kernels, launches=1):
-    """HBM bytes per call of the named kernels (FETCH_SIZE + WRITE_SIZE per dispatch,
-    scaled, times `launches` dispatches of each per call) from the committed counter
-    summary of this workload, or None when any of them is missing there."""
+    """HBM bytes per call of the named kernels (bytes read + WRITE_SIZE per dispatch, times
+    `launches` dispatches of each per call) from the committed counter summary of this
+    workload, or None when any of them is missing there. Bytes read are the per-size
+    request counts (READ_BYTES) where the summary has them, else the scaled FETCH_SIZE."""
     path = os.path.join(ROOT, "profiles", TRAFFIC_FILES.get(workload, "-"))
     if not os.path.exists(path):
         return None
@@ -177,10 +197,13 @@ def traffic_from_profile(workload, kernels, launches=1):
         f = line.split()
         if len(f) == 4 and f[0] == "traffic_bytes" and f[1] in kernels:
             got[(f[1], f[2])] = float(f[3])
-    want = {(k, c) for k in kernels for c in ("FETCH_SIZE", "WRITE_SIZE")}
-    if not want <= set(got):
-        return None
-    return round(sum(got[k] for k in want) * launches)
+    total = 0.0
+    for k in kernels:
+        read = got.get((k, "READ_BYTES"), got.get((k, "FETCH_SIZE")))
+        if read is None or (k, "WRITE_SIZE") not in got:
+            return None
+        total += read + got[(k, "WRITE_SIZE")]
+    return round(total * launches)
 
 
 def log(msg):
@@ -199,27 +222,41 @@ def calibrate_counters(dev):
 
 class Marks:
     """A one-element bitwise-not launched between timed regions, so a kernel trace of this
-    run can be cut into exactly the replays each figure of the line comes from."""
+    run can be cut into exactly the replays each figure of the line comes from. It is
+    launched once at construction: the first launch of a torch kernel in a process loads
+    its code, and that load slowed the GPU work timed right after it (the Mixtral prefill
+    layer 654 -> 770 us, for the first region only)."""
 
     def __init__(self, dev):
         self.buf = torch.zeros(1, dtype=torch.int32, device=dev)
+        self()
+        torch.cuda.synchronize()
 
     def __call__(self):
         self.buf.bitwise_not_()
 
 
 def timed_regions(graphs, steps, warmup, dev):
-    """{name: ms per replay} of each (name, graph): every graph warmed first, then each
-    timed in turn with HIP events on the current stream, a marker dispatch before the first
-    region and after each."""
+    """{name: ms per replay} of each (name, graph): each graph gets `warmup` replays, then
+    replays for WARM_MS more, right before `steps` replays between HIP events on the
+    current stream, bracketed by a marker dispatch on each side. The timed replays so run
+    in the GPU's sustained state under that load: after a few ms of replays the prefill
+    layers ran up to 14 % slower than after 150 ms (Mixtral 742 vs 651 us), while the
+    decode layer runs about 1.5 % faster before its clocks settle (10.14 vs 10.30 us)."""
+    mark = Marks(dev)
+    spans = []
     for _name, graph in graphs:
         for _ in range(warmup):
             graph.replay()
-    torch.cuda.synchronize()
-    mark = Marks(dev)
-    spans = []
-    mark()
-    for _name, graph in graphs:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        for _ in range(int(WARM_MS / max(a.elapsed_time(b), 1e-3))):
+            graph.replay()
+        torch.cuda.synchronize()
+        mark()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(steps):
@@ -450,9 +487,9 @@ def bench_prefill(args, spec):
     # launch rate, not the GPU's (the stages are idempotent). Marked regions: 0 the layer,
     # 1 gate/up, 2 down, 3 reduce.
     rep = 10
-    graphs = [("layer", capture(run_layer))] + [
-        (st, capture(lambda st=st: [run_stage(st) for _ in range(rep)]))
-        for st in ("gate_up", "down", "reduce")]
+    stages = [(st, capture(lambda st=st: [run_stage(st) for _ in range(rep)]))
+              for st in ("gate_up", "down", "reduce")]
+    graphs = [("layer", capture(run_layer))] + stages
     timed = timed_regions(graphs, steps, args.warmup, dev)
     ms = timed["layer"]
     stage_ms = {st: timed[st] / rep for st in ("gate_up", "down", "reduce")}
@@ -520,7 +557,7 @@ def bench_prefill(args, spec):
             if bound == "mfma" else
             {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
              "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    roof.update({"traffic": traffic_from_profile(args.workload, PF_KERNELS),
+    roof.update({"traffic": traffic_from_profile(args.workload, PF_KERNELS, len(prepared)),
                  "kernels": "prefill_gate_up + prefill_down + prefill_reduce",
                  "flops_per_call": flops, "bytes_per_call": wbytes + act_bytes,
                  "measured_mfma_peak_tflops": peak_meas,
