@@ -86,10 +86,13 @@ __device__ __forceinline__ RunInfo run_of(const int64_t* __restrict__ tbl, int b
     }
     if ((b - first) % R != 0) return r;
   }
-  int n = 1;
-  while (n < R && b + n < n_blocks && tbl[2 * (b + n)] == me) ++n;
+  // run length in one probe: lane l checks block b + 1 + l; the run ends at the first
+  // lane whose block is past the table, another expert's, or R blocks on
+  const int lane = threadIdx.x & 63;
+  const int c = b + 1 + lane;
+  const uint64_t stop = __ballot(lane >= R - 1 || c >= n_blocks || tbl[2 * c] != me);
   r.lead = 1;
-  r.nblk = n;
+  r.nblk = __ffsll((unsigned long long)stop);      // 1 + the number of blocks after b
   return r;
 }
 
