@@ -1008,12 +1008,17 @@ def main():
         torch.cuda.synchronize()
         routed_graph = capture(routed_layer)
 
+    # layer 0 launched L times in one graph: its 19.5 MB stay in the 256 MB MALL, so this is
+    # the warm figure beside the line's cold one (every layer's weights from HBM)
+    warm_graph = capture(lambda _l, s: (gate_up(0, s), down(0, s)))
+
     # warm every graph, then time each in its own marked region (region 0: the layer,
-    # 1: gate/up alone, 2: down alone, 3: the routed layer)
-    graphs = [("layer", full), ("gate_up", gu_only), ("down", dn_only)]
+    # 1: gate/up alone, 2: down alone, 3: layer 0 repeated (weights in MALL), 4: the routed
+    # layer)
+    graphs = [("layer", full), ("gate_up", gu_only), ("down", dn_only), ("warm", warm_graph)]
     if routed_layer is not None:
         graphs.append(("routed", routed_graph))
-    if fused is not None:                    # region 4 (or 3): the one-launch layer
+    if fused is not None:                    # the last region: the one-launch layer
         graphs.append(("fused", capture(fused)))
     ms = timed_regions(graphs, args.steps, args.warmup, dev)
     ms_two = ms["layer"]
@@ -1173,6 +1178,8 @@ def main():
                                 if fused is not None else
                                 f"decode layer ({GU_KERNEL} + {DN_KERNEL})"),
                      "two_launch_us_per_layer": round(ms_two * 1000.0 / L, 3),
+                     # the same launches over layer 0 only, its weights resident in the MALL
+                     "warm_in_mall_us_per_layer": round(ms["warm"] * 1000.0 / L, 3),
                      "eager_us_per_layer": eager,
                      "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
