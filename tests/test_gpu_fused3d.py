@@ -151,3 +151,39 @@ def test_a_call_split_into_token_chunks_gives_the_same_bits(monkeypatch):
     torch.cuda.synchronize()
     assert len(parts) == -(-T // step) and sum(parts) == T
     assert torch.equal(split, whole)
+
+
+@pytest.mark.parametrize("E,H,I,k", [(6, 160, 96, 3), (16, 320, 224, 4), (8, 256, 256, 2)])
+def test_only_the_routed_experts_rows_are_read(E, H, I, k):
+    """The load-time check (random bytes in every non-routed expert's rows, the outputs
+    bitwise equal) passes, with and without padded K loops."""
+    from vaayu_amd.fused3d import check_routed_reads
+    print(f"routed-read check E={E} H={H} I={I} k={k}", flush=True)
+    mod = to_module(random_layer(E, H, I, seed=80 + E))
+    ok, why = check_routed_reads(mod, k)
+    assert ok, why
+
+
+def test_a_poisoned_neighbour_expert_does_not_reach_the_output():
+    """H = 160 and I = 96 pad the K loops to 256 and 128: each routed expert's last gate/up
+    and down rows run into the next expert's first row. Experts 1 and 3 are never routed
+    and hold 0xFF (NaN) scales, all-ones codes and NaN biases; the output equals the clean
+    layer's bit for bit and is finite."""
+    E, H, I, T = 4, 160, 96, 12
+    clean = random_layer(E, H, I, seed=90)
+    bad = {n: t.clone() for n, t in clean.items()}
+    for e in (1, 3):
+        for n in ("gu_scales", "dn_scales", "gu_blocks", "dn_blocks"):
+            bad[n][e] = 0xFF
+        bad["gu_bias"][e] = float("nan")
+        bad["dn_bias"][e] = float("nan")
+    g = torch.Generator().manual_seed(91)
+    idx = torch.stack([torch.tensor([0, 2])[torch.randperm(2, generator=g)] for _ in range(T)])
+    w = torch.randn(T, 2, generator=g).softmax(-1)
+    x = torch.randn(T, H, generator=g).bfloat16().to(DEV)
+    want = to_module(clean).forward(x, idx, w.to(DEV))
+    got = to_module(bad).forward(x, idx, w.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, want)
+    check(got, F3.fused3d_experts(x.cpu(), idx, w, **clean))

@@ -15,7 +15,9 @@
 // column j, row 2j+1 = up column j), scales [E, 2I, H/32] E8M0; down blocks [E, H, I/32, 16],
 // scales [E, H, I/32]; biases fp32 [E, 2I] and [E, H]. The K loop runs to K rounded up to a
 // whole step (128): the activations carry zeros there (the caller pads x and h), and the
-// weight codes read past a row's end are finite, so the tail adds exact zeros; reads past
+// units past a row's K, which lie in the next row (at an expert's last row, the next
+// expert's, whatever its bytes), take a zero scale and so zero weights: the tail adds
+// exact zeros and no byte outside the routed experts' rows reaches an output. Reads past
 // the tensors' ends return zeros (buffer bounds).
 #include "prefill_kernels.hpp"
 
@@ -26,13 +28,14 @@ namespace vaayu {
 __device__ __forceinline__ Role make_role_pitched(const char* codes, const char* sc,
                                                   uint32_t code_pitch, uint32_t sc_pitch,
                                                   const char* codes_end, const char* sc_end,
-                                                  int n) {
+                                                  int k, int n) {
   Role r;
   r.row_bytes = code_pitch;
   r.row_groups = sc_pitch;
   r.codes = rsrc(codes, (uint32_t)min<int64_t>(codes_end - codes, 0xFFFFFFF0ll));
   r.sc = rsrc(sc, (uint32_t)min<int64_t>(sc_end - sc, 0xFFFFFFF0ll));
   r.bf16_mask = 0u;
+  r.kc_end = (uint32_t)k;
   r.n = n;
   r.gshift = 5;                 // E8M0 scale per 32 codes
   r.rshift = 0;
@@ -67,8 +70,9 @@ __device__ __forceinline__ void oss_gate_up_run(const Item& it, const Fused3DArg
   const char* sc = (const char*)p.tbl[2 * it.b + 1];
   const uint32_t row_b = (uint32_t)p.k / 2, row_s = (uint32_t)p.k / 32;
   const Role role[2] = {
-      make_role_pitched(pk, sc, 2 * row_b, 2 * row_s, p.codes_end, p.sc_end, nn),
-      make_role_pitched(pk + row_b, sc + row_s, 2 * row_b, 2 * row_s, p.codes_end, p.sc_end, nn)};
+      make_role_pitched(pk, sc, 2 * row_b, 2 * row_s, p.codes_end, p.sc_end, p.k, nn),
+      make_role_pitched(pk + row_b, sc + row_s, 2 * row_b, 2 * row_s, p.codes_end, p.sc_end,
+                        p.k, nn)};
   const float* bias = (const float*)p.btbl[it.b];
   const float bg = bias[2 * nn], bu = bias[2 * nn + 1];
   const int64_t* rrow = p.rows + (int64_t)it.b * 16;
@@ -109,7 +113,7 @@ __device__ __forceinline__ void oss_down_run(const Item& it, const Fused3DArgs& 
   const char* pk = (const char*)p.tbl[2 * it.b];
   const char* sc = (const char*)p.tbl[2 * it.b + 1];
   const Role role[1] = {make_role_pitched(pk, sc, (uint32_t)p.k / 2, (uint32_t)p.k / 32,
-                                          p.codes_end, p.sc_end, nn)};
+                                          p.codes_end, p.sc_end, p.k, nn)};
   const float bd = ((const float*)p.btbl[it.b])[nn];
   const int64_t* rrow = p.rows + (int64_t)it.b * 16;
   AStage<KS, S> a;

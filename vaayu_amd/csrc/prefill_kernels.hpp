@@ -235,6 +235,7 @@ struct Role {
   rsrc_t codes, sc;
   uint32_t row_bytes, row_groups;
   uint32_t bf16_mask;
+  uint32_t kc_end;             // the row's K: E8M0 scales of units at or past it read as 0
   int n, gshift, rshift;       // rshift: log2(rows per scale block), 0 but for e4m3
 };
 
@@ -249,6 +250,7 @@ __device__ __forceinline__ Role make_role(const char* pk, int64_t w_off, const c
   r.codes = rsrc(pk + w_off * 4, r.row_bytes * (uint32_t)rows);
   r.sc = rsrc(sc + s_off * sb, r.row_groups * (uint32_t)(rows >> rshift) * sb);
   r.bf16_mask = opaque(sc_dt == DT_BF16 ? 0xFFFFFFFFu : 0u);
+  r.kc_end = (uint32_t)k;
   r.n = n;
   r.gshift = gshift;
   r.rshift = rshift;
@@ -260,9 +262,18 @@ __device__ __forceinline__ BStep b_load(const Role& r, int kc) {
   BStep o;
   o.q = bload16(r.codes, (uint32_t)r.n * r.row_bytes + (uint32_t)kc * BITS / 8);
   const uint32_t si = (uint32_t)(r.n >> r.rshift) * r.row_groups + ((uint32_t)kc >> r.gshift);
-  if constexpr (SW == 32) o.s = __builtin_amdgcn_raw_buffer_load_b32(r.sc, si * 4u, 0, 0);
-  else if constexpr (SW == 8) o.s = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r.sc, si, 0, 0);
-  else o.s = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r.sc, si * 2u, 0, 0);
+  if constexpr (SW == 32) {
+    o.s = __builtin_amdgcn_raw_buffer_load_b32(r.sc, si * 4u, 0, 0);
+  } else if constexpr (SW == 8) {
+    // A unit past the row's K (a K loop padded to whole steps) would take the next row's
+    // codes and scale, which may be another expert's and any byte; its scale reads as 0,
+    // which makes every weight of the unit +-0 (the e2m1 dequant clears the codes'
+    // magnitudes for a zero scale), so the padding adds exact zeros whatever lies there.
+    const uint32_t sb = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r.sc, si, 0, 0);
+    o.s = (uint32_t)kc < r.kc_end ? sb : 0u;
+  } else {
+    o.s = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r.sc, si * 2u, 0, 0);
+  }
   return o;
 }
 

@@ -78,6 +78,16 @@ class Fused3DExperts:
     def _end(self, t):
         return t.data_ptr() + t.numel() * t.element_size()
 
+    def tensors(self) -> dict:
+        """The six per-expert tensors the kernels read, by constructor argument name."""
+        return {"gate_up_blocks": self.gu_codes, "gate_up_scales": self.gu_scales,
+                "gate_up_bias": self.gu_bias, "down_blocks": self.dn_codes,
+                "down_scales": self.dn_scales, "down_bias": self.dn_bias}
+
+    def like(self, tensors: dict) -> "Fused3DExperts":
+        """The same module (alpha, limit) over other tensors of the same geometry."""
+        return Fused3DExperts(**tensors, alpha=self.alpha, limit=self.limit)
+
     def tables(self, expert_ids):
         """The call's device tables from ONE pinned copy: (gate/up table, down table,
         gate/up bias table, down bias table, rows, slot order, n_blocks)."""
@@ -168,3 +178,73 @@ class Fused3DExperts:
             self._end(self.dn_scales), st)
         _lib.check(rc, "vaayu_fused3d_down")
         pk._reduce(y, order, out, top_k)
+
+
+# ── load-time check: the kernels read only the routed experts' rows ───────────────────────
+
+def check_routed_reads(experts, top_k: int, seed: int = 0) -> tuple:
+    """Show on random inputs that only the routed experts' rows reach the output
+    (the contract of vaayu/routed_fused3d.py:241-345). Returns (passed, reason).
+
+    For M = 1 and M = max(2, E // (2 top_k)) tokens with random routing: run `experts`,
+    then run a copy of it whose every NON-routed expert row, in all six tensors, holds
+    random bytes (NaN / Inf bf16 and fp32 patterns and E8M0 0xFF included, which is what
+    an unread row may hold), and require bitwise-equal outputs. Fails closed: a call that
+    routes every expert (nothing left to fill), a difference, or any exception gives
+    (False, reason). The copy costs one layer's tensors of device memory for the check."""
+    E, H, dev = experts.E, experts.H, experts.device
+    g = torch.Generator().manual_seed(seed)
+    m_multi = max(2, E // (2 * max(1, int(top_k))))
+    try:
+        for m in (1, m_multi):
+            x = torch.randn(m, H, generator=g).to(device=dev, dtype=torch.bfloat16)
+            ids = torch.stack([torch.randperm(E, generator=g)[:top_k] for _ in range(m)])
+            w = torch.randn(m, top_k, generator=g).softmax(-1).to(dev)
+            routed = sorted(set(ids.reshape(-1).tolist()))
+            if len(routed) >= E:
+                return False, (f"vacuous at M={m}: all {E} experts were routed, so no row "
+                               f"was left to fill")
+            out_real = experts.forward(x, ids, w)
+            keep = torch.tensor(routed, device=dev)
+            filled = {}
+            for name, t in experts.tensors().items():
+                raw = t.contiguous().view(torch.uint8)
+                noise = torch.randint(0, 256, tuple(raw.shape), dtype=torch.uint8,
+                                      generator=g).to(dev)
+                noise[keep] = raw[keep]
+                filled[name] = noise.view(t.dtype).reshape(t.shape)
+            out_bad = experts.like(filled).forward(x, ids, w)
+            if not torch.equal(out_real, out_bad):
+                diff = (out_real.float() - out_bad.float()).abs().max().item()
+                return False, (f"non-routed expert rows change the output at M={m} "
+                               f"(max|diff| {diff:.3e}): the kernels read rows they were "
+                               f"not routed to")
+        return True, (f"non-routed expert rows do not change the output at M=1 and "
+                      f"M={m_multi}")
+    except Exception as e:  # noqa: BLE001 -- fails closed; the reason is returned
+        return False, f"self-check raised {type(e).__name__}: {e}"
+
+
+_ROUTED_VERDICTS: dict = {}
+
+
+def geometry_key(experts, top_k: int) -> tuple:
+    return (experts.E, experts.H, experts.I, experts.alpha, experts.limit, int(top_k))
+
+
+def routed_reads_verdict(experts, top_k: int, name: str = "this layer") -> bool:
+    """`check_routed_reads` once per geometry (experts, sizes, SwiGLU constants, top_k),
+    with one line printed when it is decided: the kernels are used for a geometry that
+    passes; a failing one is a WARNING, and its layers keep the experts module's own
+    forward (vaayu/routed_fused3d.py:348-386 decides routed delivery the same way)."""
+    key = geometry_key(experts, top_k)
+    if key not in _ROUTED_VERDICTS:
+        ok, why = check_routed_reads(experts, top_k)
+        _ROUTED_VERDICTS[key] = ok
+        if ok:
+            print(f"[Vaayu-MoE] fused-3D kernels ON for {name}'s geometry ({why}): only "
+                  f"the routed experts' rows are read.")
+        else:
+            print(f"[Vaayu-MoE] WARNING: fused-3D kernels OFF for {name}'s geometry -- "
+                  f"{why}. Its layers keep the experts module's own forward.")
+    return _ROUTED_VERDICTS[key]
