@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 8
+#define VAAYU_ABI_VERSION 9
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -281,6 +281,14 @@ int32_t vaayu_decode_fused_sync_words(int32_t n_pairs, const vaayu_geom *geom, i
  * [blocks * 256] fp32 receives one sum per lane. 2 * 16 * 16 * 32 * 16 * iters * 4 * blocks
  * FLOPs per launch: the benchmark's measured bf16 matrix-core peak. */
 int vaayu_probe_mfma(float *out, int32_t blocks, int32_t iters, void *stream);
+
+/* Measurement only (no counterpart in the reference): d [16 row_tiles, 16 col_tiles] fp32
+ * = a [16 row_tiles, k] times b [16 col_tiles, k]^T (both bf16, row-major), accumulated in
+ * fp32 by v_mfma_f32_16x16x32_bf16 in the prefill kernels' K order (per 128-element step,
+ * quarter q of MFMA i takes elements 32q + 8i .. +8). For measuring their accumulation error
+ * against exact sums; k a positive multiple of 128. */
+int vaayu_probe_mfma_sum(const void *a, const void *b, float *d, int32_t k, int32_t row_tiles,
+                         int32_t col_tiles, void *stream);
 
 #ifdef __cplusplus
 }

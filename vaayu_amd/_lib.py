@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -21,7 +21,7 @@ EXPORTS = ("vaayu_abi_version", "vaayu_last_error", "vaayu_decode_gate_up", "vaa
            "vaayu_route_topk", "vaayu_gdn_rule", "vaayu_gdn_conv_update", "vaayu_gdn_gated_norm",
            "vaayu_fused3d_gate_up", "vaayu_fused3d_down", "vaayu_router_logits",
            "vaayu_decode_noalloc", "vaayu_decode_noalloc_scratch_bytes", "vaayu_probe_mfma",
-           "vaayu_decode_fused", "vaayu_decode_fused_sync_words")
+           "vaayu_decode_fused", "vaayu_decode_fused_sync_words", "vaayu_probe_mfma_sum")
 
 
 class Geom(ctypes.Structure):
@@ -75,6 +75,7 @@ def _bind(lib):
                                                 vp]),
         "vaayu_decode_noalloc_scratch_bytes": (ctypes.c_int64, []),
         "vaayu_probe_mfma": (ctypes.c_int, [vp, i32, i32, vp]),
+        "vaayu_probe_mfma_sum": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp]),
         "vaayu_decode_fused": (ctypes.c_int, [vp, vp, vp, i32, vp, vp, vp, i32, gp, i32, i32,
                                               i32, i32, vp]),
         "vaayu_decode_fused_sync_words": (ctypes.c_int32, [i32, gp, i32, i32]),
