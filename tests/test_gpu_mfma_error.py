@@ -7,7 +7,7 @@ N(0, 1) activations (K 7168, the DeepSeek-V3 gate/up loop) and against SwiGLU
 intermediates (K 2048 and 14336, the DeepSeek-V3 and Mixtral down loops). With Q the sum
 of squares of the partial sums after each 32-product MFMA, the error v - S is unbiased
 with rms about 0.7 * 2^-24 sqrt(Q), and it rounds to another bf16 than S in a few outputs
-in 10,000: the figures the numerics notes quote, printed as one JSON line per K."""
+in 10,000; the figures are printed as one JSON line per K."""
 import json
 
 import numpy as np
