@@ -631,16 +631,8 @@ def bench_fused3d(args, spec):
     with torch.cuda.graph(graph):
         run()
     steps = max(1, args.steps // 5)
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(steps):
-        graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / steps
+    # timed in the sustained state, as the packed-expert prefill layers are
+    ms = timed_regions([("layer", graph)], steps, args.warmup, dev)["layer"]
     flops = 2 * T * K * 3 * H * I
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"layer {ms * 1000:.1f} us = {ms * 1000 / T:.3f} us/token; {tflops:.1f} TFLOP/s "

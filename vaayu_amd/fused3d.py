@@ -97,15 +97,18 @@ class Fused3DExperts:
         n, top_k = eidx.shape
         order, live, counts = pk._prefill_plan(eidx)
         nblk = (counts + _BLOCK_M - 1) // _BLOCK_M
-        blk_end = nblk.cumsum(0)
-        n_blocks = int(blk_end[-1])
+        n_blocks = int(nblk.sum())
+        # experts laid out in the XCD-balancing order of the packed-expert prefill tables
+        lay = torch.tensor(pk._block_order(nblk.tolist()), dtype=torch.int64)
+        first_blk = torch.empty_like(nblk)
+        first_blk[lay] = nblk[lay].cumsum(0) - nblk[lay]
         owner = torch.repeat_interleave(torch.arange(live.numel()), counts)
         first_row = counts.cumsum(0) - counts
-        dest = (((blk_end - nblk) * _BLOCK_M)[owner] + torch.arange(order.numel())
+        dest = ((first_blk * _BLOCK_M)[owner] + torch.arange(order.numel())
                 - first_row[owner])
         rows = torch.full((n_blocks * _BLOCK_M,), -1, dtype=torch.int64)
         rows[dest] = order
-        e_blk = torch.repeat_interleave(live, nblk)
+        e_blk = torch.repeat_interleave(live[lay], nblk[lay])
         st = self._stride
         cols = [torch.stack([self.gu_codes.data_ptr() + e_blk * st["gu_c"],
                              self.gu_scales.data_ptr() + e_blk * st["gu_s"]], 1).reshape(-1),
