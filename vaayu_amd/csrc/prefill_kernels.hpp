@@ -319,10 +319,117 @@ __device__ __forceinline__ void k_step(const char* cur,
 // them. At the end of the step one barrier (its wait also covers the direct loads) makes
 // step t+1's rows visible and frees step t's tile. Requests past the last step re-read the
 // last step (no branches in the loop body; their results are not used).
+// ── short runs: two K steps per barrier ──────────────────────────────────────────────────
+//
+// Runs of up to kPairS blocks take the K loop two steps at a time: a tile (sized for one
+// step of a full run) holds two steps' activation rows, and each pair of steps starts by sending
+// the next pair's rows (to the other tile) and requesting the next pair's codes, then
+// computes its two steps (each step's B operands built right before its MFMAs) and ends at
+// one barrier. That barrier waits for the rows just sent; the codes, requested after them,
+// stay in flight until the next pair's barrier, so they have two steps to arrive, and half
+// as many barriers stand in a short run's K loop. Every output takes the same MFMAs in the
+// same order as in run_k, so the bits are the same whatever the run's length.
+// A pair tile holds two steps of S*16 rows, inside the kernels' tiles of one step of a
+// full run (kRunGateUp or kRunDown blocks): S <= half a run.
+constexpr int kPairS = 4;
+static_assert(2 * kPairS <= kRunGateUp && 2 * kPairS <= kRunDown,
+              "a pair of steps must fit one LDS tile");
+
+template <int F, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void one_step(const char* buf, const BStep (&raw)[NR],
+                                         const Role (&role)[NR], const Masks& M, int q, int m,
+                                         f32x4 (&acc)[NR][S]) {
+  constexpr int CPU = 128 / CodeBits<F>::value;
+  constexpr int NM = CPU / 8;
+  constexpr int KS = 4 * CPU;
+  float sn[NR];
+  GroupK kn[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    sn[r] = applied_scale<F, ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask));
+    kn[r] = group_of<F>(sn[r]);
+  }
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    uint4 b[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) b[r] = operand_i<F, ACT>(raw[r].q, kn[r], sn[r], M, i);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const uint4 av = a_read<KS, S, CPU>(buf, s, i, q, m);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) acc[r][s] = mfma16<ACT>(av, b[r], acc[r][s]);
+    }
+  }
+}
+
+template <int F, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void pair_step(const char* cur, char* nxt, rsrc_t src,
+                                          const AStage<512 / CodeBits<F>::value, S>& a, int t,
+                                          int T, int last, const BStep (&c0)[NR],
+                                          const BStep (&c1)[NR], BStep (&n0)[NR],
+                                          BStep (&n1)[NR], const Role (&role)[NR],
+                                          const Masks& M, int q, int m, f32x4 (&acc)[NR][S]) {
+  constexpr int BITS = CodeBits<F>::value;
+  constexpr int CPU = 128 / BITS;
+  constexpr int KS = 4 * CPU;
+  using A = AStage<KS, S>;
+  const int k2 = min((t + 2) * KS, last), k3 = min((t + 3) * KS, last);
+  a_issue<KS, S>(a, src, nxt, k2);
+  a_issue<KS, S>(a, src, nxt + A::BYTES, k3);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    n0[r] = b_load<BITS, SW>(role[r], k2 + q * CPU);
+    n1[r] = b_load<BITS, SW>(role[r], k3 + q * CPU);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  one_step<F, ACT, SW, NR, S>(cur, c0, role, M, q, m, acc);
+  if (t + 1 < T) one_step<F, ACT, SW, NR, S>(cur + A::BYTES, c1, role, M, q, m, acc);
+  __syncthreads();
+}
+
+template <int F, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void run_k_pairs(const Role (&role)[NR], rsrc_t src,
+                                            const AStage<512 / CodeBits<F>::value, S>& a,
+                                            char* lds0, char* lds1, int K, int q, int m,
+                                            f32x4 (&acc)[NR][S]) {
+  constexpr int BITS = CodeBits<F>::value;
+  constexpr int CPU = 128 / BITS;
+  constexpr int KS = 4 * CPU;
+  using A = AStage<KS, S>;
+  static_assert(2 * S <= kRunGateUp && 2 * S <= kRunDown, "a pair of steps must fit one tile");
+  const Masks M = make_masks();
+  const int T = K / KS, last = K - KS;
+  BStep c0[NR], c1[NR], n0[NR], n1[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[r][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  a_issue<KS, S>(a, src, lds0, 0);
+  a_issue<KS, S>(a, src, lds0 + A::BYTES, min(KS, last));
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    c0[r] = b_load<BITS, SW>(role[r], q * CPU);
+    c1[r] = b_load<BITS, SW>(role[r], min(KS, last) + q * CPU);
+  }
+  __syncthreads();
+  for (int t = 0; t < T; t += 4) {
+    pair_step<F, ACT, SW, NR, S>(lds0, lds1, src, a, t, T, last, c0, c1, n0, n1, role, M, q, m, acc);
+    if (t + 2 >= T) break;
+    pair_step<F, ACT, SW, NR, S>(lds1, lds0, src, a, t + 2, T, last, n0, n1, c0, c1, role, M, q, m,
+                                 acc);
+  }
+}
+
 template <int F, int ACT, int SW, int NR, int S>
 __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
                                       const AStage<512 / CodeBits<F>::value, S>& a, char* lds0,
                                       char* lds1, int K, int q, int m, f32x4 (&acc)[NR][S]) {
+  if constexpr (S <= kPairS) {
+    run_k_pairs<F, ACT, SW, NR, S>(role, src, a, lds0, lds1, K, q, m, acc);
+    return;
+  }
   constexpr int BITS = CodeBits<F>::value;
   constexpr int CPU = 128 / BITS;
   constexpr int NM = CPU / 8;
