@@ -297,10 +297,19 @@ __device__ __forceinline__ void k_step(const char* cur,
     sn[r] = applied_scale<F, ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask));
     kn[r] = group_of<F>(sn[r]);
   }
+  // Gate/up reads each A operand two slots before its MFMAs (it feeds two roles, so the read
+  // is worth the registers); down reads it right before (measured: Mixtral down +3 to +7 %
+  // with any read-ahead, gate/up -1 to -3 %).
+  constexpr int AH = NR == 2 ? 2 : 0;
+  uint4 ar[AH + 1];
+#pragma unroll
+  for (int g = 0; g < AH && g < SLOTS; ++g) ar[g] = a_read<KS, S, CPU>(cur, g / NM, g % NM, q, m);
 #pragma unroll
   for (int g = 0; g < SLOTS; ++g) {
     const int s = g / NM, i = g % NM;
-    const uint4 av = a_read<KS, S, CPU>(cur, s, i, q, m);
+    if (g + AH < SLOTS)
+      ar[(g + AH) % (AH + 1)] = a_read<KS, S, CPU>(cur, (g + AH) / NM, (g + AH) % NM, q, m);
+    const uint4 av = ar[g % (AH + 1)];
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r][s] = mfma16<ACT>(av, o[r][i], acc[r][s]);
 #pragma unroll
