@@ -68,11 +68,13 @@ TRAFFIC_FILES = {"qwen3-decode": "decode_qwen3_b1_traffic.txt",
                  "dsv3-decode": "decode_dsv3_b1_traffic.txt",
                  "dsv3-prefill": "prefill_dsv3_2048_traffic.txt",
                  "mixtral-prefill": "prefill_mixtral_512_traffic.txt",
-                 "qwen3-prefill": "prefill_qwen3_256_traffic.txt"}
+                 "qwen3-prefill": "prefill_qwen3_256_traffic.txt",
+                 "gptoss-20b-prefill": "fused3d_gptoss20b_prefill_2048_traffic.txt"}
 GU_KERNEL = "mfma_gate_up_kernel"     # the decode gate/up kernel bf16 activations run
 DN_KERNEL = "mfma_down_kernel"
 PF_KERNELS = ("prefill_gate_up_kernel", "prefill_down_kernel", "prefill_reduce_kernel")
-TRAFFIC_KERNELS = (GU_KERNEL, DN_KERNEL) + PF_KERNELS
+F3_KERNELS = ("fused3d_gate_up_kernel", "fused3d_down_kernel", "prefill_reduce_kernel")
+TRAFFIC_KERNELS = (GU_KERNEL, DN_KERNEL) + PF_KERNELS + F3_KERNELS[:2]
 
 
 def _csv_rows(d, suffix):
@@ -630,6 +632,7 @@ def bench_fused3d(args, spec):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         run()
+    calibrate_counters(dev)
     steps = max(1, args.steps // 5)
     # timed in the sustained state, as the packed-expert prefill layers are
     ms = timed_regions([("layer", graph)], steps, args.warmup, dev)["layer"]
@@ -679,7 +682,7 @@ def bench_fused3d(args, spec):
                    "top_k": K, "tokens": T, "parallelism": "none (one GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": traffic_from_profile(args.workload, F3_KERNELS),
                      "kernels": "fused3d_gate_up + fused3d_down + prefill_reduce",
                      "flops_per_call": flops, "weight_bytes": wbytes},
         "parity": parity, "cpu_baseline": cpu,
