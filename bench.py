@@ -451,26 +451,27 @@ def bench_prefill(args, spec):
     prepared = []
     for ei, wi, k in calls:
         plan = pk._prefill_plan(ei)
-        tbl, rows, order, n_blocks = pk._prefill_tables(ei, plan, blobs, dev)
-        tbl, rows, order = tbl.clone(), rows.clone(), order.clone()     # off the table ring
+        tbl, rows, order, n_blocks, work = pk._prefill_tables(ei, plan, blobs, dev)
+        tbl, rows, order, work = tbl.clone(), rows.clone(), order.clone(), work.clone()
         h = torch.empty(T * k, I, dtype=torch.bfloat16, device=dev)
         y = torch.empty(T * k, H, dtype=torch.float32, device=dev)
         out = torch.empty(T, H, dtype=torch.float32, device=dev)
-        prepared.append((tbl, rows, order, n_blocks, k, wi, h, y, out, int(plan[1].numel())))
+        prepared.append((tbl, rows, order, n_blocks, work, k, wi, h, y, out,
+                         int(plan[1].numel())))
     torch.cuda.synchronize()
 
     def run_layer():
-        for tbl, rows, order, n_blocks, k, wi, h, y, out, _live in prepared:
-            pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h)
-            pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y)
+        for tbl, rows, order, n_blocks, work, k, wi, h, y, out, _live in prepared:
+            pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h, work=work)
+            pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y, work=work)
             pk._reduce(y, order, out, k)
 
     def run_stage(stage):
-        for tbl, rows, order, n_blocks, k, wi, h, y, out, _live in prepared:
+        for tbl, rows, order, n_blocks, work, k, wi, h, y, out, _live in prepared:
             if stage == "gate_up":
-                pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h)
+                pk._gate_up_g(x, tbl, rows, n_blocks, k, geom, sc, h=h, work=work)
             elif stage == "down":
-                pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y)
+                pk._down_g(h, tbl, rows, n_blocks, wi, geom, sc, y=y, work=work)
             else:
                 pk._reduce(y, order, out, k)
 
@@ -509,7 +510,7 @@ def bench_prefill(args, spec):
 
     # parity: a few tokens against the oracle (each token's output depends on its own
     # routing only)
-    outs = [p[8] for p in prepared]
+    outs = [p[9] for p in prepared]            # each call's out
     n_chk = 2 if H * I > 4e6 else 8
     tok = torch.randperm(T, generator=cg)[:n_chk].tolist()
     cpu_blob = {}
@@ -616,7 +617,7 @@ def bench_fused3d(args, spec):
     logits = torch.randn(T, E, generator=cg)
     top, eidx = torch.topk(logits, K, dim=-1)        # gpt-oss: top-k logits, softmax of them
     w = torch.softmax(top, dim=-1).to(dev)
-    tables = tuple(t.clone() if isinstance(t, torch.Tensor) else t for t in mod.tables(eidx))
+    tables = tuple(t.clone() if hasattr(t, "clone") else t for t in mod.tables(eidx))
     xp = torch.zeros(T, mod.Hp, dtype=torch.bfloat16, device=dev)
     xp[:, :H] = x
     h = torch.zeros(T * K, mod.Ip, dtype=torch.bfloat16, device=dev)

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 9
+#define VAAYU_ABI_VERSION 10
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -85,23 +85,38 @@ int vaayu_decode_down(const void *h, const int64_t *table, const void *routing_w
  * x     [tokens, hidden] contiguous (dtype `act`: bf16 or fp16)
  * rows  int64 [n_blocks * 16]: row ids token*top_k + slot, -1 pads a block
  * table int64 [n_blocks * 2]: (packed address, scale address) of each block's expert
+ * work  int64 [n_slots * 8]: the launch's work items (no counterpart in the reference,
+ *       whose launch covers every block): work[k * 8 + x] = b * 32 + S for a run of S
+ *       blocks of one expert starting at table block b (1 <= S <= the run length
+ *       vaayu_prefill_run_blocks(0) gives), or -1; each run is computed for every N tile on
+ *       XCD x. Every block of the table must lie in exactly one run; an entry that does
+ *       not fit the table computes nothing. n_slots in [0, n_blocks].
  * h     [tokens * top_k, inter] (dtype `act`); padding rows are never written
  * x and h rows are addressed with 32-bit byte offsets: a launch whose tables could hold
  * rows past 0xF0000000 bytes (n_blocks * 16 / top_k tokens of x) is refused with -2; split
  * such a call into token chunks (every row's arithmetic is independent of its launch-mates). */
-int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *table, void *h,
-                          int32_t n_blocks, int32_t top_k, const vaayu_geom *geom, int32_t act,
+int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *table,
+                          const int64_t *work, int32_t n_slots, void *h, int32_t n_blocks,
+                          int32_t top_k, const vaayu_geom *geom, int32_t act,
                           int32_t scale_dtype, void *stream);
 
 /* Prefill, down stage. Replaces `_down_g` / `_down_grouped`
  * (vaayu/packed_expert_kernels.py:735-749, 218-247).
  * y [tokens * top_k, hidden] fp32 <- fl32(round(h[row].Wd) * routing_weights[row]),
  * rounded again when w_round != 0; routing_weights contiguous [tokens * top_k].
+ * work / n_slots as for vaayu_prefill_gate_up, with runs of at most
+ * vaayu_prefill_run_blocks(1) blocks.
  * Refused with -2 when n_blocks * 16 rows of h would reach past 0xF0000000 bytes. */
 int vaayu_prefill_down(const void *h, const int64_t *rows, const int64_t *table,
-                       const void *routing_weights, int32_t rw_dtype, float *y,
-                       int32_t n_blocks, const vaayu_geom *geom, int32_t act,
-                       int32_t scale_dtype, int32_t w_round, void *stream);
+                       const int64_t *work, int32_t n_slots, const void *routing_weights,
+                       int32_t rw_dtype, float *y, int32_t n_blocks, const vaayu_geom *geom,
+                       int32_t act, int32_t scale_dtype, int32_t w_round, void *stream);
+
+/* The longest run (16-row blocks) a work item of the grouped kernels takes: which = 0
+ * gate/up (vaayu_prefill_gate_up, vaayu_fused3d_gate_up), 1 down (vaayu_prefill_down,
+ * vaayu_fused3d_down); -1 otherwise. No counterpart in the reference (its BLOCK_M plan
+ * has no runs). */
+int32_t vaayu_prefill_run_blocks(int32_t which);
 
 /* Prefill reduce. Replaces `_reduce` / `_reduce_kernel` (vaayu/packed_expert_kernels.py:752-757,
  * 250-260): out[t] = sum over k, in `order`'s order, of y[order[t*top_k + k]], fp32 from 0.
@@ -223,7 +238,8 @@ int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
  * [E, 2I, H/32, 16] (row 2j gate column j, row 2j+1 up column j) + E8M0 scales [E, 2I, H/32];
  * down blocks [E, H, I/32, 16] + scales [E, H, I/32]. rows / n_blocks: the prefill block plan
  * (16 row ids per block, row id = token * top_k + slot, -1 padding); tbl [n_blocks, 2]: the
- * block's expert (codes address, scales address); btbl [n_blocks]: its fp32 bias address.
+ * block's expert (codes address, scales address); btbl [n_blocks]: its fp32 bias address;
+ * work / n_slots: the launch's work list, as for vaayu_prefill_gate_up / vaayu_prefill_down.
  * codes_end / scales_end: the tensors' ends (reads past them return zeros). H, I multiples
  * of 32; hidden_pad / inter_pad: multiples of 128 at least H / I, the row pitches of x and
  * h, whose padding columns must hold zeros. */
@@ -232,7 +248,8 @@ int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
  * gate clipped above at `limit`, up to [-limit, limit], s = gate / (1 + exp(-alpha gate)),
  * h = fma(s, up, s). x [tokens, hidden_pad] bf16. */
 int vaayu_fused3d_gate_up(const void *x, const int64_t *rows, const int64_t *tbl,
-                          const int64_t *btbl, void *h, int32_t n_blocks, int32_t top_k,
+                          const int64_t *btbl, const int64_t *work, int32_t n_slots,
+                          void *h, int32_t n_blocks, int32_t top_k,
                           int32_t hidden, int32_t hidden_pad, int32_t inter, int32_t inter_pad,
                           const void *codes_end, const void *scales_end, float alpha,
                           float limit, void *stream);
@@ -240,7 +257,8 @@ int vaayu_fused3d_gate_up(const void *x, const int64_t *rows, const int64_t *tbl
 /* y [tokens * top_k, hidden] fp32 <- bf16((h_row . W_down^T + b) * gammas[row]) per live row;
  * `vaayu_prefill_reduce` then sums each token's slots in ascending expert id. */
 int vaayu_fused3d_down(const void *h, const int64_t *rows, const int64_t *tbl,
-                       const int64_t *btbl, const float *gammas, float *y, int32_t n_blocks,
+                       const int64_t *btbl, const int64_t *work, int32_t n_slots,
+                       const float *gammas, float *y, int32_t n_blocks,
                        int32_t top_k, int32_t hidden, int32_t inter, int32_t inter_pad,
                        const void *codes_end, const void *scales_end, void *stream);
 

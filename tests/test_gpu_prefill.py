@@ -51,9 +51,9 @@ def _stages(x, eidx, w, blobs, h=None, y=None):
     blob = blobs[int(plan[1][0])]
     geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
     top_k = eidx.shape[1]
-    tbl, rows, order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
-    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=h)
-    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, y=y)
+    tbl, rows, order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=h, work=work)
+    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, y=y, work=work)
     torch.cuda.synchronize()
     return h, y, order, plan
 
@@ -329,12 +329,12 @@ def test_the_library_refuses_a_launch_past_its_offset_range():
     buf = torch.zeros(64, dtype=torch.int64, device="cuda")
     huge = (0xF0000000 // (2 * QWEN[1])) // 16 + 1                 # h rows one block past
     rc = lib.vaayu_prefill_down(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
-                                2, buf.data_ptr(), huge, g, 0, 0, 0,
+                                0, buf.data_ptr(), 2, buf.data_ptr(), huge, g, 0, 0, 0,
                                 _lib.stream_ptr(buf.device))
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     tokens_over = (0xF0000000 // (2 * QWEN[0])) + 1                 # x rows one token past
     rc = lib.vaayu_prefill_gate_up(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
-                                   buf.data_ptr(), -(-tokens_over // 16), 1, g, 0, 0,
-                                   _lib.stream_ptr(buf.device))
+                                   buf.data_ptr(), 0, buf.data_ptr(), -(-tokens_over // 16), 1,
+                                   g, 0, 0, _lib.stream_ptr(buf.device))
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     torch.cuda.synchronize()

@@ -1,8 +1,8 @@
 """The prefill tables' host layout (vaayu_amd/packed_expert_kernels.py: _prefill_layout,
-_block_order) on the CPU: every routed row once, each expert's rows in ascending order over
+_prefill_work) on the CPU: every routed row once, each expert's rows in ascending order over
 contiguous blocks padded with -1 (the block structure of vaayu/packed_expert_kernels.py:
-691-717), experts in the XCD-balancing order, which spreads the kernels' work over the
-eight XCDs more evenly than ascending expert ids on the benchmark's routing."""
+691-717), and work lists that cover every block once, in runs of one expert, and spread
+the kernels' work over the eight XCDs."""
 import numpy as np
 import torch
 
@@ -15,16 +15,11 @@ def _zipf(tokens, experts, top_k, seed):
     return torch.multinomial(p.expand(tokens, experts), top_k, replacement=False, generator=g)
 
 
-def _xcd_work(order, blocks):
-    """Work per XCD of a table laid out in `order`, by the kernels' mapping (the runs that
-    start in group G of 8 blocks go to XCD G % 8) and `_run_cost`."""
-    work, pos = np.zeros(8), 0
-    for i in order:
-        b = int(blocks[i])
-        for first in range(0, b, 8):
-            work[((pos + first) // 8) % 8] += pk._run_cost(min(8, b - first))
-        pos += b
-    return work
+def _runs(work):
+    """(XCD, first block, length) of each entry of a work list."""
+    w = work.reshape(-1, 8)
+    return [(x, int(e) >> 5, int(e) & 31) for k in range(w.shape[0]) for x in range(8)
+            for e in [w[k, x]] if int(e) >= 0]
 
 
 def test_every_row_once_in_its_experts_blocks():
@@ -54,24 +49,38 @@ def test_every_row_once_in_its_experts_blocks():
             at += int(blocks[i])
 
 
-def test_order_is_deterministic_and_heavy_experts_lead():
-    blocks = [3, 12, 1, 8, 30, 2, 1, 7]
-    a = pk._block_order(blocks)
-    assert a == pk._block_order(list(blocks))
-    assert a[:3] == [1, 3, 4], "experts of 8 or more blocks first, in ascending id"
-    assert sorted(a) == list(range(len(blocks)))
+def test_work_lists_cover_every_block_once_in_runs_of_one_expert():
+    for seed in range(8):
+        g = torch.Generator().manual_seed(seed)
+        blocks = torch.randint(1, 40, (int(torch.randint(1, 300, (1,), generator=g)),),
+                               generator=g).tolist()
+        starts = np.cumsum([0] + blocks)
+        for run in (8, 16):
+            work, n_slots = pk._prefill_work(blocks, run)
+            assert work.dtype == torch.int64 and work.numel() == n_slots * 8
+            runs = _runs(work)
+            n_runs = sum(-(-b // run) for b in blocks)
+            assert len(runs) == n_runs and n_slots == -(-n_runs // 8)
+            seen = np.zeros(int(starts[-1]), dtype=int)
+            for _x, first, n in runs:
+                assert 1 <= n <= run
+                e = int(np.searchsorted(starts, first, side="right")) - 1
+                assert (first - starts[e]) % run == 0, "runs start R blocks apart"
+                assert first + n <= starts[e + 1], "a run stays inside its expert"
+                seen[first:first + n] += 1
+            assert (seen == 1).all(), "every block in exactly one run"
+            assert work.tolist() == pk._prefill_work(list(blocks), run)[0].tolist()
 
 
-def test_the_order_spreads_the_work_over_the_xcds():
-    """DeepSeek-V3 2048-token Zipf routing (top-8 of 256) and other seeds: the busiest XCD
-    holds at most 5 % more work than the mean, where ascending expert ids give up to 21 %."""
-    worst_asc = 0.0
+def test_work_lists_spread_the_work_over_the_xcds():
+    """DeepSeek-V3 2048-token Zipf routing (top-8 of 256) and other seeds, runs of 8 and 16
+    blocks: the busiest XCD holds at most 5 % more work (`_run_cost`) than the mean."""
     for seed in range(6):
         eidx = _zipf(2048, 256, 8, seed)
         _order, live, counts = pk._prefill_plan(eidx)
         blocks = ((counts + 15) // 16).tolist()
-        asc = _xcd_work(range(len(blocks)), blocks)
-        bal = _xcd_work(pk._block_order(blocks), blocks)
-        worst_asc = max(worst_asc, asc.max() / asc.mean())
-        assert bal.max() / bal.mean() < 1.05
-    assert worst_asc > 1.15, "premise: ascending ids leave some seed unbalanced"
+        for run in (8, 16):
+            load = np.zeros(8)
+            for x, _first, n in _runs(pk._prefill_work(blocks, run)[0]):
+                load[x] += pk._run_cost(n)
+            assert load.max() / load.mean() < 1.05, (seed, run, load)

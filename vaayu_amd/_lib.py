@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -21,7 +21,8 @@ EXPORTS = ("vaayu_abi_version", "vaayu_last_error", "vaayu_decode_gate_up", "vaa
            "vaayu_route_topk", "vaayu_gdn_rule", "vaayu_gdn_conv_update", "vaayu_gdn_gated_norm",
            "vaayu_fused3d_gate_up", "vaayu_fused3d_down", "vaayu_router_logits",
            "vaayu_decode_noalloc", "vaayu_decode_noalloc_scratch_bytes", "vaayu_probe_mfma",
-           "vaayu_decode_fused", "vaayu_decode_fused_sync_words", "vaayu_probe_mfma_sum")
+           "vaayu_decode_fused", "vaayu_decode_fused_sync_words", "vaayu_probe_mfma_sum",
+           "vaayu_prefill_run_blocks")
 
 
 class Geom(ctypes.Structure):
@@ -50,9 +51,11 @@ def _bind(lib):
         "vaayu_last_error": (ctypes.c_char_p, []),
         "vaayu_decode_gate_up": (ctypes.c_int, [vp, vp, vp, i32, gp, i32, i32, vp]),
         "vaayu_decode_down": (ctypes.c_int, [vp, vp, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
-        "vaayu_prefill_gate_up": (ctypes.c_int, [vp, vp, vp, vp, i32, i32, gp, i32, i32, vp]),
+        "vaayu_prefill_gate_up": (ctypes.c_int, [vp, vp, vp, vp, i32, vp, i32, i32, gp, i32,
+                                                 i32, vp]),
         "vaayu_prefill_down": (ctypes.c_int,
-                               [vp, vp, vp, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
+                               [vp, vp, vp, vp, i32, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
+        "vaayu_prefill_run_blocks": (ctypes.c_int32, [i32]),
         "vaayu_prefill_reduce": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp]),
         "vaayu_dequant_blob": (ctypes.c_int, [vp, vp, i32, vp, i32, i64, i32, i32, vp]),
         "vaayu_dequant_fp8_block": (ctypes.c_int, [vp, vp, i32, vp, i32, i64, i64, i64, i64, vp]),
@@ -65,11 +68,11 @@ def _bind(lib):
                                                  i32, i32, i32, vp]),
         "vaayu_gdn_gated_norm": (ctypes.c_int, [vp, vp, vp, vp, vp, i64, i32, ctypes.c_float,
                                                 i32, i32, i32, i32, vp]),
-        "vaayu_fused3d_gate_up": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32,
-                                                 i32, vp, vp, ctypes.c_float, ctypes.c_float,
-                                                 vp]),
-        "vaayu_fused3d_down": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32,
-                                              vp, vp, vp]),
+        "vaayu_fused3d_gate_up": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32,
+                                                 i32, i32, i32, vp, vp, ctypes.c_float,
+                                                 ctypes.c_float, vp]),
+        "vaayu_fused3d_down": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
+                                              i32, i32, vp, vp, vp]),
         "vaayu_router_logits": (ctypes.c_int, [vp, vp, i32, vp, i32, i32, i32, i32, vp]),
         "vaayu_decode_noalloc": (ctypes.c_int, [vp, vp, vp, i32, vp, i32, gp, i32, i32, i32,
                                                 vp]),

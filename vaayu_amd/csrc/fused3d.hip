@@ -46,6 +46,7 @@ struct Fused3DArgs {
   const int64_t* rows;
   const int64_t* tbl;           // [n_blocks, 2] (codes, scales) of each block's expert
   const int64_t* btbl;          // [n_blocks] its bias
+  const int64_t* work;          // the work list (prefill_kernels.hpp: item_here)
   const char* codes_end;
   const char* sc_end;
   int n_blocks, n_tiles, top_k;
@@ -148,15 +149,24 @@ __device__ __forceinline__ void oss_down_run(const Item& it, const Fused3DArgs& 
     case 4: CALL(4); break; case 5: CALL(5); break; case 6: CALL(6); break;          \
     case 7: CALL(7); break; case 8: CALL(8); break; default: break;                 \
   }
+#define VAAYU_F3D_BY_S16(CALL)                                                      \
+  switch (it.S) {                                                                   \
+    case 1: CALL(1); break; case 2: CALL(2); break; case 3: CALL(3); break;          \
+    case 4: CALL(4); break; case 5: CALL(5); break; case 6: CALL(6); break;          \
+    case 7: CALL(7); break; case 8: CALL(8); break; case 9: CALL(9); break;          \
+    case 10: CALL(10); break; case 11: CALL(11); break; case 12: CALL(12); break;    \
+    case 13: CALL(13); break; case 14: CALL(14); break; case 15: CALL(15); break;    \
+    case 16: CALL(16); break; default: break;                                       \
+  }
 
 __global__ void __launch_bounds__(64 * kWaves)
 fused3d_gate_up_kernel(Fused3DArgs p, const void* __restrict__ x, void* __restrict__ h) {
   __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / 4)];
   __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / 4)];
   __shared__ int rid_s[kRunGateUp * 16];
-  const Item it = item_here<kRunGateUp>(p.tbl, p.n_blocks, p.n_tiles);
+  const Item it = item_here<kRunGateUp>(p.work, p.n_blocks, p.n_tiles);
 #define F3_GU(S_) oss_gate_up_run<S_>(it, p, x, h, lds0, lds1, rid_s)
-  VAAYU_F3D_BY_S(F3_GU)
+  VAAYU_F3D_BY_S16(F3_GU)
 #undef F3_GU
 }
 
@@ -167,13 +177,14 @@ fused3d_down_kernel(Fused3DArgs p, const void* __restrict__ h, const float* __re
   __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / 4)];
   __shared__ int rid_s[kRunDown * 16];
   __shared__ float w_s[kRunDown * 16];
-  const Item it = item_here<kRunDown>(p.tbl, p.n_blocks, p.n_tiles);
+  const Item it = item_here<kRunDown>(p.work, p.n_blocks, p.n_tiles);
 #define F3_DN(S_) oss_down_run<S_>(it, p, h, gammas, y, lds0, lds1, rid_s, w_s)
   VAAYU_F3D_BY_S(F3_DN)
 #undef F3_DN
 }
 
 #undef VAAYU_F3D_BY_S
+#undef VAAYU_F3D_BY_S16
 
 }  // namespace vaayu
 
@@ -188,49 +199,55 @@ static int fused3d_check(int n_blocks, int top_k, int k, int k_pad, int n_out) {
 }
 
 extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const int64_t* tbl,
-                                     const int64_t* btbl, void* h, int32_t n_blocks,
+                                     const int64_t* btbl, const int64_t* work, int32_t n_slots,
+                                     void* h, int32_t n_blocks,
                                      int32_t top_k, int32_t hidden, int32_t hidden_pad,
                                      int32_t inter, int32_t inter_pad, const void* codes_end,
                                      const void* scales_end, float alpha, float limit,
                                      void* stream) {
   clear_error();
-  if (!x || !rows || !tbl || !btbl || !h || !codes_end || !scales_end)
+  if (!x || !rows || !tbl || !btbl || !work || !h || !codes_end || !scales_end)
     return set_error(-1, "null pointer argument");
+  if (n_slots < 0 || n_slots > n_blocks) return set_error(-2, "n_slots must be in [0, n_blocks]");
   if (int rc = fused3d_check(n_blocks, top_k, hidden, hidden_pad, inter)) return rc;
   if (inter_pad < inter) return set_error(-2, "h's row pitch is below the intermediate size");
   if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * hidden_pad, 0))
     return set_error(-2, why);
   if (n_blocks == 0) return 0;
   Fused3DArgs p;
-  p.rows = rows; p.tbl = tbl; p.btbl = btbl;
+  p.rows = rows; p.tbl = tbl; p.btbl = btbl; p.work = work;
   p.codes_end = (const char*)codes_end; p.sc_end = (const char*)scales_end;
   p.n_blocks = n_blocks; p.n_tiles = (inter + kTileN - 1) / kTileN; p.top_k = top_k;
   p.k = hidden; p.k_pad = hidden_pad; p.n_out = inter; p.out_pitch = inter_pad;
   p.alpha = alpha; p.limit = limit;
-  const dim3 grid((unsigned)items_for<kRunGateUp>(n_blocks, p.n_tiles)), block(64 * kWaves);
+  if (n_slots == 0) return 0;
+  const dim3 grid = work_grid(n_slots, p.n_tiles), block(64 * kWaves);
   hipLaunchKernelGGL(fused3d_gate_up_kernel, grid, block, 0, (hipStream_t)stream, p, x, h);
   return check_launch("fused-3D gate/up");
 }
 
 extern "C" int vaayu_fused3d_down(const void* h, const int64_t* rows, const int64_t* tbl,
-                                  const int64_t* btbl, const float* gammas, float* y,
+                                  const int64_t* btbl, const int64_t* work, int32_t n_slots,
+                                  const float* gammas, float* y,
                                   int32_t n_blocks, int32_t top_k, int32_t hidden,
                                   int32_t inter, int32_t inter_pad, const void* codes_end,
                                   const void* scales_end, void* stream) {
   clear_error();
-  if (!h || !rows || !tbl || !btbl || !gammas || !y || !codes_end || !scales_end)
+  if (!h || !rows || !tbl || !btbl || !work || !gammas || !y || !codes_end || !scales_end)
     return set_error(-1, "null pointer argument");
+  if (n_slots < 0 || n_slots > n_blocks) return set_error(-2, "n_slots must be in [0, n_blocks]");
   if (int rc = fused3d_check(n_blocks, top_k, inter, inter_pad, hidden)) return rc;
   if (const char* why = rows_out_of_reach(n_blocks, 1, 0, 2ll * inter_pad))
     return set_error(-2, why);
   if (n_blocks == 0) return 0;
   Fused3DArgs p;
-  p.rows = rows; p.tbl = tbl; p.btbl = btbl;
+  p.rows = rows; p.tbl = tbl; p.btbl = btbl; p.work = work;
   p.codes_end = (const char*)codes_end; p.sc_end = (const char*)scales_end;
   p.n_blocks = n_blocks; p.n_tiles = (hidden + kTileN - 1) / kTileN; p.top_k = top_k;
   p.k = inter; p.k_pad = inter_pad; p.n_out = hidden; p.out_pitch = hidden;
   p.alpha = 0.f; p.limit = 0.f;
-  const dim3 grid((unsigned)items_for<kRunDown>(n_blocks, p.n_tiles)), block(64 * kWaves);
+  if (n_slots == 0) return 0;
+  const dim3 grid = work_grid(n_slots, p.n_tiles), block(64 * kWaves);
   hipLaunchKernelGGL(fused3d_down_kernel, grid, block, 0, (hipStream_t)stream, p, h, gammas, y);
   return check_launch("fused-3D down");
 }

@@ -52,19 +52,21 @@ const char* prefill_unsupported(const vaayu_geom* g, int act, int sc) {
 using namespace vaayu;
 
 extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const int64_t* table,
-                                     void* h, int32_t n_blocks, int32_t top_k,
-                                     const vaayu_geom* g, int32_t act, int32_t scale_dtype,
-                                     void* stream) {
+                                     const int64_t* work, int32_t n_slots, void* h,
+                                     int32_t n_blocks, int32_t top_k, const vaayu_geom* g,
+                                     int32_t act, int32_t scale_dtype, void* stream) {
   clear_error();
-  if (!x || !rows || !table || !h || !g) return set_error(-1, "null pointer argument");
+  if (!x || !rows || !table || !work || !h || !g) return set_error(-1, "null pointer argument");
   if (n_blocks <= 0 || top_k <= 0) return set_error(-1, "n_blocks / top_k must be positive");
+  if (n_slots < 0 || n_slots > n_blocks) return set_error(-1, "n_slots must be in [0, n_blocks]");
   if (scale_dtype < 0 || scale_dtype > 3) return set_error(-1, "scale dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
   if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * g->hidden, 0))
     return set_error(-2, why);
   const PrefillArgs p{n_blocks, (g->inter + kTileN - 1) / kTileN, top_k, g->hidden, g->inter,
                       log2_of(g->group),
-                      g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype};
+                      g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype,
+                      work, n_slots};
   hipStream_t st = (hipStream_t)stream;
   if (g->format != VAAYU_FMT_INT) {
     const int rc = prefill_gate_up_formats(x, rows, table, h, p, g, act, st);
@@ -82,13 +84,15 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
 }
 
 extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int64_t* table,
+                                  const int64_t* work, int32_t n_slots,
                                   const void* routing_weights, int32_t rw_dtype, float* y,
                                   int32_t n_blocks, const vaayu_geom* g, int32_t act,
                                   int32_t scale_dtype, int32_t w_round, void* stream) {
   clear_error();
-  if (!h || !rows || !table || !routing_weights || !y || !g)
+  if (!h || !rows || !table || !work || !routing_weights || !y || !g)
     return set_error(-1, "null pointer argument");
   if (n_blocks <= 0) return set_error(-1, "n_blocks must be positive");
+  if (n_slots < 0 || n_slots > n_blocks) return set_error(-1, "n_slots must be in [0, n_blocks]");
   if (scale_dtype < 0 || scale_dtype > 3 || rw_dtype < 0 || rw_dtype > 2)
     return set_error(-1, "scale / routing-weight dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
@@ -96,7 +100,8 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
     return set_error(-2, why);
   const PrefillArgs p{n_blocks, (g->hidden + kTileN - 1) / kTileN, 1, g->hidden, g->inter,
                       log2_of(g->group),
-                      g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype};
+                      g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype,
+                      work, n_slots};
   hipStream_t st = (hipStream_t)stream;
   if (g->format != VAAYU_FMT_INT) {
     const int rc = prefill_down_formats(h, rows, table, routing_weights, rw_dtype, y, p, g, act,
@@ -112,6 +117,12 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
 #undef DN2
 #undef DN
   return check_launch("prefill down");
+}
+
+// The run length (blocks) the work lists of the grouped kernels may hold: which = 0
+// gate/up (prefill and fused-3D), 1 down.
+extern "C" int32_t vaayu_prefill_run_blocks(int32_t which) {
+  return which == 0 ? kRunGateUp : which == 1 ? kRunDown : -1;
 }
 
 extern "C" int vaayu_prefill_reduce(const float* y, const int64_t* order, float* out,

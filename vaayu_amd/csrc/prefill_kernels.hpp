@@ -41,12 +41,11 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // ── run-tiled grouped GEMM ─────────────────────────────────────────────────────────────
 //
 // A work item is a RUN of up to R consecutive 16-row blocks of one expert (the table lists
-// each expert's blocks contiguously) times kTileN weight rows (N); R is kRunGateUp for gate/up,
-// whose two roles hold twice the accumulators, and kRunDown for down. An expert's blocks
-// form runs of R from its first block on (an expert of k blocks takes ceil(k / R) runs), so
-// a block can tell from the table alone whether it leads a run (its predecessor is another
-// expert, or it lies a multiple of R blocks past its expert's first block) and how long the
-// run is; items of non-leading blocks exit at once. The kernels branch once on the run's
+// each expert's blocks contiguously) times kTileN weight rows (N); R is kRunGateUp for
+// gate/up and kRunDown for down. The host lists the runs (an expert's blocks in runs of R
+// from its first block on) in a work list, so only workgroups with work are launched: a
+// workgroup launched only to find that it has nothing to do holds a whole CU (one gate/up
+// workgroup fills one) for a few memory round trips. The kernels branch once on the run's
 // length S to a K loop compiled for that S.
 //
 // Per K step (4 units of codes per weight row) the block stages the run's activation rows
@@ -55,62 +54,26 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // shared by up to R*16 rows. The A operand of sub-tile s comes from LDS with the same K-slot
 // map as B (quarter q of the wave, MFMA i: codes [q*CPU + 8i, +8) of the step).
 //
-// XCD mapping: linear workgroup id L runs on XCD L % 8. Blocks are grouped by b / R and group
-// G is placed on XCD G % 8, with all of a group's N tiles consecutive in that XCD's order, so
-// the items that share a run's activation rows (those of its leading block) share an L2.
+// XCD mapping: linear workgroup id L runs on XCD L % 8; the work list gives each XCD its
+// runs, with all N tiles of a run consecutive in that XCD's order, so the items that share
+// a run's activation rows share an L2.
+//
+// Runs of more than 8 blocks (gate/up) take each K step as the MFMAs of the step, then the
+// dequant of the next step's operands, so the two steps' operands are never live together
+// and the 16-block path's 128 accumulators fit two waves per SIMD.
 
-constexpr int kRunGateUp = 8;    // blocks per run, gate/up (two roles of accumulators)
+constexpr int kRunGateUp = 16;   // blocks per run, gate/up
 constexpr int kRunDown = 8;      // blocks per run, down
 constexpr int kWaves = 8;        // waves per workgroup, 16 weight rows (N) each
 constexpr int kTileN = 16 * kWaves;
 
-struct RunInfo {
-  int lead;       // 1 if this item computes
-  int nblk;       // blocks in the run
-};
-
-template <int R>
-__device__ __forceinline__ RunInfo run_of(const int64_t* __restrict__ tbl, int b, int n_blocks) {
-  RunInfo r{0, 0};
-  if (b >= n_blocks) return r;
-  const int64_t me = tbl[2 * b];
-  if (b > 0 && tbl[2 * (b - 1)] == me) {
-    // not its expert's first block: find the first (64 table entries a probe, one per
-    // lane), and lead only R, 2R, ... blocks on from it
-    const int lane = threadIdx.x & 63;
-    int first = -1;
-    for (int base = b - 1; first < 0; base -= 64) {
-      const int c = base - lane;
-      const uint64_t other = __ballot(c < 0 || tbl[2 * c] != me);
-      if (other) first = base - (__ffsll((unsigned long long)other) - 1) + 1;
-    }
-    if ((b - first) % R != 0) return r;
-  }
-  // run length in one probe: lane l checks block b + 1 + l; the run ends at the first
-  // lane whose block is past the table, another expert's, or R blocks on
-  const int lane = threadIdx.x & 63;
-  const int c = b + 1 + lane;
-  const uint64_t stop = __ballot(lane >= R - 1 || c >= n_blocks || tbl[2 * c] != me);
-  r.lead = 1;
-  r.nblk = __ffsll((unsigned long long)stop);      // 1 + the number of blocks after b
-  return r;
-}
-
-// (block b, N tile) of linear workgroup id L.
-template <int R>
-__device__ __forceinline__ void item_of(int L, int n_tiles, int& b, int& tile) {
-  const int xcd = L & 7, j = L >> 3;
-  const int per_group = R * n_tiles;                     // items of one group of blocks
-  const int g = j / per_group, w = j - g * per_group;
-  b = (g * 8 + xcd) * R + w / n_tiles;
-  tile = w % n_tiles;
-}
-
-template <int R>
-__host__ __device__ inline int items_for(int n_blocks, int n_tiles) {
-  const int groups = (n_blocks + R - 1) / R;
-  return ((groups + 7) / 8) * 8 * R * n_tiles;
-}
+// Work list: one int64 entry per (slot k, XCD x) at work[k * 8 + x], b * 32 + S for the
+// run of S blocks that starts at table block b (S <= the kernel's run length), -1 for none.
+// Workgroup L runs on XCD x = L % 8 and takes N tile j % n_tiles of the run in slot
+// j / n_tiles of its XCD (j = L / 8), so all N tiles of a run share one XCD's L2 and only
+// workgroups with work are launched. The host chooses which runs go to which XCD.
+constexpr int kXcds = 8;
+constexpr int64_t kRunShift = 5;
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -318,6 +281,51 @@ __device__ __forceinline__ void k_step(const char* cur,
   }
 }
 
+// The step of runs longer than 8 blocks: this step's MFMAs first, then the next step's
+// dequant, so the operands of the two steps are never live together.
+template <int F, int ACT, int SW, int NR, int S>
+__device__ __forceinline__ void k_step_split(const char* cur,
+                                             const uint4 (&o)[NR][128 / CodeBits<F>::value / 8],
+                                             const BStep (&raw)[NR], const Role (&role)[NR],
+                                             uint4 (&on)[NR][128 / CodeBits<F>::value / 8],
+                                             const Masks& M, int q, int m, f32x4 (&acc)[NR][S]) {
+  constexpr int CPU = 128 / CodeBits<F>::value;
+  constexpr int NM = CPU / 8;
+  constexpr int KS = 4 * CPU;
+  constexpr int SLOTS = S * NM, JOBS = NR * NM;
+  constexpr int AH = 2;
+  uint4 ar[AH + 1];
+#pragma unroll
+  for (int g = 0; g < AH; ++g) ar[g] = a_read<KS, S, CPU>(cur, g / NM, g % NM, q, m);
+#pragma unroll
+  for (int g = 0; g < SLOTS; ++g) {
+    const int s = g / NM, i = g % NM;
+    if (g + AH < SLOTS)
+      ar[(g + AH) % (AH + 1)] = a_read<KS, S, CPU>(cur, (g + AH) / NM, (g + AH) % NM, q, m);
+    const uint4 av = ar[g % (AH + 1)];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r][s] = mfma16<ACT>(av, o[r][i], acc[r][s]);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, AH + 1, 0);
+#pragma unroll
+  for (int g = 0; g < SLOTS; ++g) {
+    __builtin_amdgcn_sched_group_barrier(0x008, NR, 0);
+    if (g + AH + 1 < SLOTS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float sn[NR];
+  GroupK kn[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    sn[r] = applied_scale<F, ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask));
+    kn[r] = group_of<F>(sn[r]);
+  }
+#pragma unroll
+  for (int j = 0; j < JOBS; ++j)
+    on[j / NM][j % NM] = operand_i<F, ACT>(raw[j / NM].q, kn[j / NM], sn[j / NM], M, j % NM);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // The K loop of one run: NR roles sharing the activation rows (gate/up: 2, down: 1), S
 // sub-tiles of 16 rows; acc[r][s] is the 16x16 fp32 tile of role r, sub-tile s.
 //
@@ -445,6 +453,11 @@ __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
   constexpr int KS = 4 * CPU;
   const Masks M = make_masks();
   const int last = K - KS;
+#define KSTEP(...)                                                                    \
+  do {                                                                                \
+    if constexpr (S > 8) k_step_split<F, ACT, SW, NR, S>(__VA_ARGS__);                \
+    else k_step<F, ACT, SW, NR, S>(__VA_ARGS__);                                      \
+  } while (0)
   uint4 oa[NR][NM], ob[NR][NM];
   BStep raw[NR];
 #pragma unroll
@@ -470,33 +483,41 @@ __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
     // scheduling barriers keep the next step's loads ahead of this step's MFMAs
     a_issue<KS, S>(a, src, lds1, k0 + KS);
     __builtin_amdgcn_sched_barrier(0);
-    k_step<F, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
+    KSTEP(lds0, oa, raw, role, ob, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 2 * KS, last) + q * CPU);
     __syncthreads();
     // step k0 + KS (tile lds1, operands ob) -> step k0 + 2 KS (tile lds0, operands oa)
     a_issue<KS, S>(a, src, lds0, min(k0 + 2 * KS, last));
     __builtin_amdgcn_sched_barrier(0);
-    k_step<F, ACT, SW, NR, S>(lds1, ob, raw, role, oa, M, q, m, acc);
+    KSTEP(lds1, ob, raw, role, oa, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 3 * KS, last) + q * CPU);
     __syncthreads();
   }
   if (k0 < K)                                      // an odd number of steps: the last one
-    k_step<F, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
+    KSTEP(lds0, oa, raw, role, ob, M, q, m, acc);
+#undef KSTEP
 }
 
 struct Item {
   int b, tile, S;
 };
 
-// This workgroup's run and N tile, or S = 0 when it has none.
+// This workgroup's run and N tile, or S = 0 when its slot holds none (or an entry that
+// does not fit the table: such an entry computes nothing).
 template <int R>
-__device__ __forceinline__ Item item_here(const int64_t* tbl, int n_blocks, int n_tiles) {
+__device__ __forceinline__ Item item_here(const int64_t* __restrict__ work, int n_blocks,
+                                          int n_tiles) {
+  const int L = blockIdx.x, x = L % kXcds, j = L / kXcds;
+  const int k = j / n_tiles;
   Item it;
-  item_of<R>(blockIdx.x, n_tiles, it.b, it.tile);
-  const RunInfo run = run_of<R>(tbl, it.b, n_blocks);
-  it.S = run.lead ? run.nblk : 0;
+  it.tile = j - k * n_tiles;
+  const int64_t e = work[(int64_t)k * kXcds + x];
+  const int64_t b = e >> kRunShift, S = e & ((1 << kRunShift) - 1);
+  const bool ok = e >= 0 && S >= 1 && S <= R && b + S <= n_blocks;
+  it.b = ok ? (int)b : 0;
+  it.S = ok ? (int)S : 0;
   return it;
 }
 
@@ -611,36 +632,47 @@ __device__ __forceinline__ void down_run(const Item& it, const void* h, const in
     case 4: CALL(4); break; case 5: CALL(5); break; case 6: CALL(6); break;          \
     case 7: CALL(7); break; case 8: CALL(8); break; default: break;                 \
   }
+#define VAAYU_BY_S16(CALL)                                                         \
+  switch (it.S) {                                                                   \
+    case 1: CALL(1); break; case 2: CALL(2); break; case 3: CALL(3); break;          \
+    case 4: CALL(4); break; case 5: CALL(5); break; case 6: CALL(6); break;          \
+    case 7: CALL(7); break; case 8: CALL(8); break; case 9: CALL(9); break;          \
+    case 10: CALL(10); break; case 11: CALL(11); break; case 12: CALL(12); break;    \
+    case 13: CALL(13); break; case 14: CALL(14); break; case 15: CALL(15); break;    \
+    case 16: CALL(16); break; default: break;                                       \
+  }
 
 template <int F, int ACT, int SW>
 __global__ void __launch_bounds__(64 * kWaves)
 prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ rows,
-                       const int64_t* __restrict__ tbl, void* __restrict__ h, int n_blocks,
+                       const int64_t* __restrict__ tbl, const int64_t* __restrict__ work,
+                       void* __restrict__ h, int n_blocks,
                        int n_tiles, int top_k, int hidden, int inter, int gshift, int rshift,
                        int sc_dt, int64_t gate_w, int64_t gate_s, int64_t up_w, int64_t up_s) {
   constexpr int BITS = CodeBits<F>::value;
   __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / BITS)];
   __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / BITS)];
-  const Item it = item_here<kRunGateUp>(tbl, n_blocks, n_tiles);
+  const Item it = item_here<kRunGateUp>(work, n_blocks, n_tiles);
   __shared__ int rid_s[kRunGateUp * 16];
 #define GU_CALL(S_) gate_up_run<F, ACT, SW, S_>(it, x, rows, tbl, h, top_k, hidden, inter, gshift, \
                                             rshift, sc_dt, gate_w, gate_s, up_w, up_s, lds0, lds1, \
                                             rid_s)
-  VAAYU_BY_S8(GU_CALL)
+  VAAYU_BY_S16(GU_CALL)
 #undef GU_CALL
 }
 
 template <int F, int ACT, int SW>
 __global__ void __launch_bounds__(64 * kWaves)
 prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows,
-                    const int64_t* __restrict__ tbl, const void* __restrict__ rw, int rw_dt,
+                    const int64_t* __restrict__ tbl, const int64_t* __restrict__ work,
+                    const void* __restrict__ rw, int rw_dt,
                     float* __restrict__ y, int n_blocks, int n_tiles, int hidden, int inter,
                     int gshift, int rshift, int sc_dt, int64_t down_w, int64_t down_s,
                     int w_round) {
   constexpr int BITS = CodeBits<F>::value;
   __shared__ __align__(1024) char lds0[kRunDown * 16 * (2 * 512 / BITS)];
   __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / BITS)];
-  const Item it = item_here<kRunDown>(tbl, n_blocks, n_tiles);
+  const Item it = item_here<kRunDown>(work, n_blocks, n_tiles);
   __shared__ int rid_s[kRunDown * 16];
   __shared__ float w_s[kRunDown * 16];
 #define DN_CALL(S_) down_run<F, ACT, SW, S_>(it, h, rows, tbl, rw, rw_dt, y, hidden, inter, gshift, \
@@ -652,6 +684,7 @@ prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows
 
 #undef VAAYU_BY_S4
 #undef VAAYU_BY_S8
+#undef VAAYU_BY_S16
 
 // ── launches (one compile unit per code family instantiates them) ───────────────────
 
@@ -664,13 +697,22 @@ inline int log2_of(int v) {
 
 struct PrefillArgs {
   int n_blocks, n_tiles, top_k, hidden, inter, gshift, rshift, sc_dt;
+  const int64_t* work;    // the work list (see item_here) and its slots per XCD
+  int n_slots;
 };
+
+// Workgroups of a launch over n_slots slots of n_tiles N tiles each.
+inline dim3 work_grid(int n_slots, int n_tiles) {
+  return dim3((unsigned)((int64_t)n_slots * kXcds * n_tiles));
+}
 
 template <int F, int ACT, int SW>
 void launch_prefill_gate_up(const void* x, const int64_t* rows, const int64_t* tbl, void* h,
                             const PrefillArgs& p, const vaayu_geom* g, hipStream_t st) {
-  const dim3 grid((unsigned)items_for<kRunGateUp>(p.n_blocks, p.n_tiles)), block(64 * kWaves);
-  hipLaunchKernelGGL((prefill_gate_up_kernel<F, ACT, SW>), grid, block, 0, st, x, rows, tbl, h,
+  const dim3 grid = work_grid(p.n_slots, p.n_tiles), block(64 * kWaves);
+  if (p.n_slots == 0) return;
+  hipLaunchKernelGGL((prefill_gate_up_kernel<F, ACT, SW>), grid, block, 0, st, x, rows, tbl,
+                     p.work, h,
                      p.n_blocks, p.n_tiles, p.top_k, p.hidden, p.inter, p.gshift, p.rshift,
                      p.sc_dt, g->gate_w, g->gate_s, g->up_w, g->up_s);
 }
@@ -679,8 +721,9 @@ template <int F, int ACT, int SW>
 void launch_prefill_down(const void* h, const int64_t* rows, const int64_t* tbl, const void* rw,
                          int rw_dt, float* y, const PrefillArgs& p, const vaayu_geom* g,
                          int w_round, hipStream_t st) {
-  const dim3 grid((unsigned)items_for<kRunDown>(p.n_blocks, p.n_tiles)), block(64 * kWaves);
-  hipLaunchKernelGGL((prefill_down_kernel<F, ACT, SW>), grid, block, 0, st, h, rows, tbl, rw,
+  const dim3 grid = work_grid(p.n_slots, p.n_tiles), block(64 * kWaves);
+  if (p.n_slots == 0) return;
+  hipLaunchKernelGGL((prefill_down_kernel<F, ACT, SW>), grid, block, 0, st, h, rows, tbl, p.work, rw,
                      rw_dt, y, p.n_blocks, p.n_tiles, p.hidden, p.inter, p.gshift, p.rshift,
                      p.sc_dt, g->down_w, g->down_s, w_round);
 }

@@ -90,7 +90,7 @@ class Fused3DExperts:
 
     def tables(self, expert_ids):
         """The call's device tables from ONE pinned copy: (gate/up table, down table,
-        gate/up bias table, down bias table, rows, slot order, n_blocks)."""
+        gate/up bias table, down bias table, rows, slot order, n_blocks, work lists)."""
         eidx = expert_ids.to("cpu", torch.int64)
         if eidx.numel() and (int(eidx.min()) < 0 or int(eidx.max()) >= self.E):
             raise ValueError(f"expert ids must be in [0, {self.E})")
@@ -98,8 +98,7 @@ class Fused3DExperts:
         order, live, counts = pk._prefill_plan(eidx)
         nblk = (counts + _BLOCK_M - 1) // _BLOCK_M
         n_blocks = int(nblk.sum())
-        # experts laid out in the XCD-balancing order of the packed-expert prefill tables
-        lay = torch.tensor(pk._block_order(nblk.tolist()), dtype=torch.int64)
+        lay = torch.arange(live.numel(), dtype=torch.int64)      # ascending expert id
         first_blk = torch.empty_like(nblk)
         first_blk[lay] = nblk[lay].cumsum(0) - nblk[lay]
         owner = torch.repeat_interleave(torch.arange(live.numel()), counts)
@@ -118,13 +117,19 @@ class Fused3DExperts:
                 self.dn_bias.data_ptr() + e_blk * st["dn_b"], rows]
         slot_order = (torch.argsort(eidx, dim=1, stable=True)
                       + (torch.arange(n) * top_k)[:, None]).reshape(-1)
-        dev = pk._PF_TABLES.put(torch.cat(cols + [slot_order]), self.device)
-        sizes = [c.numel() for c in cols] + [slot_order.numel()]
+        n_cus = pk._cu_count(self.device)
+        w_gu, s_gu = pk._prefill_work(nblk[lay].tolist(), pk._run_blocks(0),
+                                      -(-self.I // 128), n_cus)
+        w_dn, s_dn = pk._prefill_work(nblk[lay].tolist(), pk._run_blocks(1),
+                                      -(-self.H // 128), n_cus)
+        parts = cols + [slot_order, w_gu, w_dn]
+        dev = pk._PF_TABLES.put(torch.cat(parts), self.device)
         out, at = [], 0
-        for s in sizes:
-            out.append(dev[at:at + s])
-            at += s
-        return (*out, n_blocks)
+        for t in parts:
+            out.append(dev[at:at + t.numel()])
+            at += t.numel()
+        work = pk.PrefillWork(out[-2], s_gu, out[-1], s_dn)
+        return (*out[:-2], n_blocks, work)
 
     def forward(self, x, expert_ids, routing_weights):
         """x [tokens, H] bf16; expert_ids [tokens, top_k] (any device; read on the host);
@@ -149,7 +154,7 @@ class Fused3DExperts:
 
     def _forward_part(self, x, expert_ids, routing_weights, out) -> None:
         T, top_k = expert_ids.shape
-        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks = self.tables(expert_ids)
+        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks, work = self.tables(expert_ids)
         if self.Hp == self.H and x.is_contiguous():
             xp = x
         else:
@@ -159,8 +164,8 @@ class Fused3DExperts:
             T * top_k, self.Ip, dtype=x.dtype, device=x.device)
         y = torch.empty(T * top_k, self.H, dtype=torch.float32, device=x.device)
         gammas = routing_weights.reshape(-1).to(torch.float32).contiguous()
-        self.launch(xp, h, y, out, (gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks), gammas,
-                    top_k)
+        self.launch(xp, h, y, out, (gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks, work),
+                    gammas, top_k)
 
     def launch(self, xp, h, y, out, tables, gammas, top_k) -> None:
         """The three kernels on prepared buffers (what `forward` runs; allocates nothing, so
@@ -168,15 +173,17 @@ class Fused3DExperts:
         h [tokens * top_k, Ip] bf16 with zero padding columns, y [tokens * top_k, H] fp32,
         out [tokens, H] fp32, `tables` from `tables()`, gammas fp32 [tokens * top_k]."""
         lib = pk._require_backend()
-        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks = tables
+        gu_t, dn_t, gu_b, dn_b, rows, order, n_blocks, work = tables
         st = _lib.stream_ptr(xp.device)
         rc = lib.vaayu_fused3d_gate_up(
-            xp.data_ptr(), rows.data_ptr(), gu_t.data_ptr(), gu_b.data_ptr(), h.data_ptr(),
+            xp.data_ptr(), rows.data_ptr(), gu_t.data_ptr(), gu_b.data_ptr(),
+            work.gate_up.data_ptr(), work.gate_up_slots, h.data_ptr(),
             n_blocks, top_k, self.H, self.Hp, self.I, self.Ip, self._end(self.gu_codes),
             self._end(self.gu_scales), self.alpha, self.limit, st)
         _lib.check(rc, "vaayu_fused3d_gate_up")
         rc = lib.vaayu_fused3d_down(
-            h.data_ptr(), rows.data_ptr(), dn_t.data_ptr(), dn_b.data_ptr(), gammas.data_ptr(),
+            h.data_ptr(), rows.data_ptr(), dn_t.data_ptr(), dn_b.data_ptr(),
+            work.down.data_ptr(), work.down_slots, gammas.data_ptr(),
             y.data_ptr(), n_blocks, top_k, self.H, self.I, self.Ip, self._end(self.dn_codes),
             self._end(self.dn_scales), st)
         _lib.check(rc, "vaayu_fused3d_down")

@@ -34,6 +34,7 @@ point, and nothing is accumulated atomically. Without the built library
 import collections
 import gc
 import itertools
+from typing import NamedTuple
 from pathlib import Path
 
 import torch
@@ -55,7 +56,6 @@ triton = _BACKEND
 _CHECK_TOL = 1e-2            # relL2 of a call's output vs its reference above which: refused
 _BK_MAX = 512
 _PF_BLOCK_M = 16             # rows per block of the prefill tables
-_PF_RUN = 8                  # blocks per run of the grouped kernels (kRunGateUp, kRunDown)
 _XCDS = 8                    # MI355X's accelerator dies: workgroup L runs on XCD L % 8
 _PF_MIN_TILE = 16
 _PF_GU_BK_MAX, _PF_DN_BK_MAX = 256, 256
@@ -679,57 +679,98 @@ def _run_cost(blocks: int) -> float:
     return 5.5 + blocks
 
 
-def _block_order(blocks) -> list:
-    """The order in which the live experts' blocks are laid out in the prefill tables, as
-    indices into `blocks` (each live expert's block count), so that the kernels' eight
-    XCDs get about equal work.
+class PrefillWork(NamedTuple):
+    """The work lists of one call's grouped launches (int64 on the device, `_prefill_work`)
+    and their slots per XCD."""
+    gate_up: torch.Tensor
+    gate_up_slots: int
+    down: torch.Tensor
+    down_slots: int
 
-    The kernels give the runs that start in group G of _PF_RUN consecutive blocks to XCD
-    G % 8. Experts of at least _PF_RUN blocks go first, in ascending id (their runs fill
-    consecutive groups, so every XCD gets its share, and the longest items start early;
-    sorting them by size measured 6 % slower on gpt-oss-20b's layer, where every expert
-    is that large). The smaller experts follow one at a time: the smallest left (the most
-    work per block) when the XCD of the next block has at most the mean work placed so
-    far, else the largest left. A row's arithmetic does not depend on where its block
-    sits, so every order gives the same bits; the reference lays experts out in ascending
-    id. On DeepSeek-V3's 2048-token Zipf routing this order takes the layer from 3537 to
-    3261 us on MI355X."""
-    sizes = [int(b) for b in blocks]
-    heavy = [i for i, b in enumerate(sizes) if b >= _PF_RUN]
-    small = sorted((i for i, b in enumerate(sizes) if b < _PF_RUN), key=lambda i: (sizes[i], i))
-    work = [0.0] * _XCDS
-    pos, out = 0, []
+    def clone(self) -> "PrefillWork":
+        return PrefillWork(self.gate_up.clone(), self.gate_up_slots, self.down.clone(),
+                           self.down_slots)
 
-    def place(i):
-        nonlocal pos
-        b = sizes[i]
-        for first in range(0, b, _PF_RUN):
-            work[((pos + first) // _PF_RUN) % _XCDS] += _run_cost(min(_PF_RUN, b - first))
+
+_RUN_BLOCKS = {}
+_CUS = {}
+
+
+def _cu_count(device) -> int:
+    """Compute units of the device (256 on MI355X)."""
+    d = torch.device(device)
+    key = d.index if d.index is not None else torch.cuda.current_device()
+    if key not in _CUS:
+        _CUS[key] = int(torch.cuda.get_device_properties(key).multi_processor_count)
+    return _CUS[key]
+
+
+def _run_blocks(which: int) -> int:
+    """Longest run (16-row blocks) a work item of the library's grouped kernel may take:
+    which = 0 gate/up (packed and fused-3D), 1 down."""
+    if which not in _RUN_BLOCKS:
+        _RUN_BLOCKS[which] = int(_require_backend().vaayu_prefill_run_blocks(which))
+    return _RUN_BLOCKS[which]
+
+
+def _run_length(blocks, run: int, n_tiles: int, n_cus: int) -> int:
+    """The run length (at most `run` blocks, halving) with the shortest estimated launch:
+    the larger of the work spread over the CUs and the longest item, by `_run_cost`. Long
+    runs share each K step's dequant among more rows; a call of few long runs (one
+    expert's 2048 rows) leaves CUs idle unless they are split (runs of 16 blocks give 128
+    work items for 256 CUs there, runs of 8 fill them)."""
+    best, best_t, r = run, None, run
+    while r >= 1:
+        n = [min(r, int(b) - f) for b in blocks for f in range(0, int(b), r)]
+        t = max(sum(_run_cost(x) for x in n) * n_tiles / n_cus,
+                _run_cost(max(n, default=0)))
+        if best_t is None or t < best_t:
+            best, best_t = r, t
+        r //= 2
+    return best
+
+
+def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
+    """(work, n_slots): the work list of one grouped launch over tables whose experts hold
+    `blocks` 16-row blocks each, in table order. Each expert's blocks form runs of up to
+    `run` blocks (or the `_run_length` for `n_tiles` N tiles on `n_cus` CUs, when given)
+    from its first block on; a run is one work item per N tile, all on one XCD (so they
+    share the run's activation rows in its L2). The runs go to the eight XCDs longest
+    first, each to the XCD with the least work so far (`_run_cost`) among those holding
+    fewer than ceil(runs / 8), and each XCD takes its runs in that order.
+    work[k * 8 + x] = first_block * 32 + length of XCD x's k-th run, or -1; n_slots is the
+    most runs an XCD holds. A row's arithmetic does not depend on its run's place or
+    length, so every choice gives the same bits."""
+    if n_tiles and n_cus:
+        run = _run_length(blocks, run, n_tiles, n_cus)
+    runs, pos = [], 0
+    for b in blocks:
+        b = int(b)
+        for first in range(0, b, run):
+            runs.append((pos + first, min(run, b - first)))
         pos += b
-        out.append(i)
-
-    for i in heavy:
-        place(i)
-    lo, hi = 0, len(small) - 1
-    while lo <= hi:
-        if work[(pos // _PF_RUN) % _XCDS] * _XCDS <= sum(work):
-            place(small[lo])
-            lo += 1
-        else:
-            place(small[hi])
-            hi -= 1
-    return out
+    cap = -(-len(runs) // _XCDS)
+    load, per = [0.0] * _XCDS, [[] for _ in range(_XCDS)]
+    for first, n in sorted(runs, key=lambda r: (-r[1], r[0])):
+        x = min((t for t in range(_XCDS) if len(per[t]) < cap), key=lambda t: (load[t], t))
+        per[x].append(first * 32 + n)
+        load[x] += _run_cost(n)
+    work = torch.full((max(cap, 0), _XCDS), -1, dtype=torch.int64)
+    for x, entries in enumerate(per):
+        if entries:
+            work[:len(entries), x] = torch.tensor(entries, dtype=torch.int64)
+    return work.reshape(-1), cap
 
 
 def _prefill_layout(plan):
     """Host tables of one call's blocks: (lay, blocks, rows). `lay` the live experts (as
-    indices into `live`) in table order (`_block_order`), `blocks` each live expert's block
-    count, `rows` [n_blocks * _PF_BLOCK_M] row ids: each expert's rows in ascending order
-    over its blocks, padded with -1 to whole blocks."""
+    indices into `live`) in table order (ascending id, as the reference lays them out),
+    `blocks` each live expert's block count, `rows` [n_blocks * _PF_BLOCK_M] row ids: each
+    expert's rows in ascending order over its blocks, padded with -1 to whole blocks."""
     order, live, counts = plan
     blocks = (counts + _PF_BLOCK_M - 1) // _PF_BLOCK_M          # per live expert
     n_blocks = int(blocks.sum())
-    lay = torch.tensor(_block_order(blocks.tolist()), dtype=torch.int64)
+    lay = torch.arange(live.numel(), dtype=torch.int64)
     first_block = torch.empty_like(blocks)
     first_block[lay] = torch.cumsum(blocks[lay], 0) - blocks[lay]
     expert_of_row = torch.repeat_interleave(torch.arange(live.numel()), counts)
@@ -742,12 +783,13 @@ def _prefill_layout(plan):
 
 
 def _prefill_tables(eidx_cpu, plan, blobs, device):
-    """The call's three tables on the device from ONE pinned copy
-    (vaayu/packed_expert_kernels.py:691-717): (tbl, rows, ord, n_blocks).
+    """The call's tables on the device from ONE pinned copy
+    (vaayu/packed_expert_kernels.py:691-717): (tbl, rows, ord, n_blocks, work).
 
     tbl   [n_blocks, 2] (packed address, scale address) of each block's expert
     rows  [n_blocks, _PF_BLOCK_M] row ids, each expert's rows padded to whole blocks with -1
-    ord   [tokens, top_k] row ids of each token's slots in ascending expert id"""
+    ord   [tokens, top_k] row ids of each token's slots in ascending expert id
+    work  the gate/up and down launches' work lists (`PrefillWork`, `_prefill_work`)"""
     _order, live, _counts = plan
     tokens, top_k = eidx_cpu.shape
     lay, blocks, rows = _prefill_layout(plan)
@@ -758,35 +800,45 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     tbl = torch.repeat_interleave(addresses[lay], blocks[lay], dim=0).reshape(-1)
     by_expert = torch.argsort(eidx_cpu, dim=1, stable=True)
     ord_ = (by_expert + top_k * torch.arange(tokens)[:, None]).reshape(-1)
-    dev = _PF_TABLES.put(torch.cat([tbl, rows, ord_]), device)
-    a, b = tbl.numel(), tbl.numel() + rows.numel()
-    return dev[:a], dev[a:b], dev[b:b + ord_.numel()], n_blocks
+    lay_geom = _layout(blobs[int(live[0])]["geom"])
+    hidden, inter = lay_geom["gate"][3], lay_geom["gate"][2]
+    n_cus = _cu_count(device)
+    w_gu, s_gu = _prefill_work(blocks[lay].tolist(), _run_blocks(0), -(-inter // 128), n_cus)
+    w_dn, s_dn = _prefill_work(blocks[lay].tolist(), _run_blocks(1), -(-hidden // 128), n_cus)
+    parts = [tbl, rows, ord_, w_gu, w_dn]
+    dev = _PF_TABLES.put(torch.cat(parts), device)
+    at = [0]
+    for t in parts:
+        at.append(at[-1] + t.numel())
+    sl = [dev[at[i]:at[i + 1]] for i in range(len(parts))]
+    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn)
 
 
-def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None):
+def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
     """h [tokens * top_k, intermediate], activation dtype: SiLU(gate) * up per live row
-    (vaayu/packed_expert_kernels.py:720-732)."""
+    (vaayu/packed_expert_kernels.py:720-732); `work` the call's `PrefillWork`."""
     lib = _require_backend()
     g = _lib.geom_struct(geom)
     if h is None:
         h = torch.empty(x.shape[0] * top_k, g.inter, dtype=x.dtype, device=x.device)
     _lib.check(lib.vaayu_prefill_gate_up(x.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
+                                         work.gate_up.data_ptr(), work.gate_up_slots,
                                          h.data_ptr(), n_blocks, top_k, g,
                                          _DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device)),
                "vaayu_prefill_gate_up")
     return h
 
 
-def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None):
+def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None, *, work):
     """y [tokens * top_k, hidden] fp32: each live row's down projection times its weight
-    (vaayu/packed_expert_kernels.py:735-749)."""
+    (vaayu/packed_expert_kernels.py:735-749); `work` the call's `PrefillWork`."""
     lib = _require_backend()
     g = _lib.geom_struct(geom)
     rw = routing_weights.reshape(-1).contiguous()
     if y is None:
         y = torch.empty(h.shape[0], g.hidden, dtype=torch.float32, device=h.device)
     _lib.check(lib.vaayu_prefill_down(h.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
-                                      rw.data_ptr(), _DTYPE_CODE[rw.dtype], y.data_ptr(),
+                                      work.down.data_ptr(), work.down_slots, rw.data_ptr(), _DTYPE_CODE[rw.dtype], y.data_ptr(),
                                       n_blocks, g, _DTYPE_CODE[h.dtype], sc,
                                       int(_rounds_weighted(rw.dtype, h.dtype)),
                                       _lib.stream_ptr(h.device)),
@@ -819,9 +871,9 @@ def _prefill_call(x, eidx_cpu, routing_weights, blobs, out, plan) -> None:
     blob = blobs[int(plan[1][0])]
     geom, sc, top_k = blob["geom"], _scale_code(blob), eidx_cpu.shape[1]
     x = x.contiguous()
-    tbl, rows, order, n_blocks = _prefill_tables(eidx_cpu, plan, blobs, x.device)
-    h = _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc)
-    y = _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc)
+    tbl, rows, order, n_blocks, work = _prefill_tables(eidx_cpu, plan, blobs, x.device)
+    h = _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, work=work)
+    y = _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, work=work)
     dense = out if out.is_contiguous() else torch.empty(out.shape, dtype=torch.float32,
                                                         device=out.device)
     _reduce(y, order, dense, top_k)
