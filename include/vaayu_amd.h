@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 10
+#define VAAYU_ABI_VERSION 11
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -105,10 +105,13 @@ int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *tab
  * y [tokens * top_k, hidden] fp32 <- fl32(round(h[row].Wd) * routing_weights[row]),
  * rounded again when w_round != 0; routing_weights contiguous [tokens * top_k].
  * work / n_slots as for vaayu_prefill_gate_up, with runs of at most
- * vaayu_prefill_run_blocks(1) blocks.
+ * vaayu_prefill_run_blocks(1) blocks; run_blocks: the longest run in `work` (calls whose
+ * runs are at most 8 blocks long take a kernel that fits two workgroups per CU). An entry
+ * longer than run_blocks computes nothing.
  * Refused with -2 when n_blocks * 16 rows of h would reach past 0xF0000000 bytes. */
 int vaayu_prefill_down(const void *h, const int64_t *rows, const int64_t *table,
-                       const int64_t *work, int32_t n_slots, const void *routing_weights,
+                       const int64_t *work, int32_t n_slots, int32_t run_blocks,
+                       const void *routing_weights,
                        int32_t rw_dtype, float *y, int32_t n_blocks, const vaayu_geom *geom,
                        int32_t act, int32_t scale_dtype, int32_t w_round, void *stream);
 
@@ -239,7 +242,8 @@ int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
  * down blocks [E, H, I/32, 16] + scales [E, H, I/32]. rows / n_blocks: the prefill block plan
  * (16 row ids per block, row id = token * top_k + slot, -1 padding); tbl [n_blocks, 2]: the
  * block's expert (codes address, scales address); btbl [n_blocks]: its fp32 bias address;
- * work / n_slots: the launch's work list, as for vaayu_prefill_gate_up / vaayu_prefill_down.
+ * work / n_slots (/ run_blocks): the launch's work list, as for vaayu_prefill_gate_up /
+ * vaayu_prefill_down.
  * codes_end / scales_end: the tensors' ends (reads past them return zeros). H, I multiples
  * of 32; hidden_pad / inter_pad: multiples of 128 at least H / I, the row pitches of x and
  * h, whose padding columns must hold zeros. */
@@ -258,7 +262,7 @@ int vaayu_fused3d_gate_up(const void *x, const int64_t *rows, const int64_t *tbl
  * `vaayu_prefill_reduce` then sums each token's slots in ascending expert id. */
 int vaayu_fused3d_down(const void *h, const int64_t *rows, const int64_t *tbl,
                        const int64_t *btbl, const int64_t *work, int32_t n_slots,
-                       const float *gammas, float *y, int32_t n_blocks,
+                       int32_t run_blocks, const float *gammas, float *y, int32_t n_blocks,
                        int32_t top_k, int32_t hidden, int32_t inter, int32_t inter_pad,
                        const void *codes_end, const void *scales_end, void *stream);
 

@@ -117,6 +117,25 @@ def test_results_do_not_depend_on_the_call_batch():
     assert torch.equal(full[5:6], one)
 
 
+def test_every_run_length_gives_the_same_bits(monkeypatch):
+    """The layer's output does not depend on how an expert's blocks are cut into runs, nor
+    on which of the two down kernels (runs of up to 8 or up to 16 blocks) takes them."""
+    import vaayu_amd.packed_expert_kernels as pk
+    E, H, I, k, T = 4, 256, 256, 1, 400
+    mod = to_module(random_layer(E, H, I, seed=3))
+    idx, w = routing(T, E, k, seed=4, skew=2.0)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(5)) * 0.5).to(torch.bfloat16)
+    outs = {}
+    for r_gu, r_dn in ((8, 8), (16, 16), (1, 12), (16, 3)):
+        monkeypatch.setattr(pk, "_run_length",
+                            lambda blocks, run, n_tiles, n_cus, r=r_gu: min(run, r))
+        monkeypatch.setattr(pk, "_down_run",
+                            lambda blocks, n_tiles, n_cus, r=r_dn: min(r, max(blocks)))
+        outs[(r_gu, r_dn)] = mod.forward(x.to(DEV), idx, w.to(DEV)).clone()
+    for key, out in outs.items():
+        assert torch.equal(out, outs[(8, 8)]), f"runs {key}"
+
+
 def test_bad_calls_raise():
     layer = random_layer(4, 128, 128, seed=60)
     mod = to_module(layer)

@@ -132,6 +132,26 @@ def test_a_token_does_not_depend_on_the_tokens_it_shares_a_call_with():
         assert torch.equal(alone[0], full[t]), f"token {t}"
 
 
+def test_every_run_length_gives_the_same_bits(monkeypatch):
+    """h and y do not depend on how an expert's blocks are cut into runs (runs of 1 to 16
+    blocks for gate/up; down's kernel for runs of up to 8 and the one for up to 16): every
+    row takes the same MFMAs in the same order."""
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, n_exp=3, tokens=300, top_k=2)
+    assert int(pk._prefill_plan(eidx)[2].max()) > 12 * 16, "premise: experts of > 12 blocks"
+    outs = {}
+    for r_gu, r_dn in ((8, 8), (16, 16), (16, 1), (4, 16), (1, 2), (3, 11)):
+        monkeypatch.setattr(pk, "_run_length",
+                            lambda blocks, run, n_tiles, n_cus, r=r_gu: min(run, r))
+        monkeypatch.setattr(pk, "_down_run",
+                            lambda blocks, n_tiles, n_cus, r=r_dn: min(r, max(blocks)))
+        h, y, _o, _p = _stages(x, eidx, w, blobs)
+        outs[(r_gu, r_dn)] = (h.clone(), y.clone())
+    h0, y0 = outs[(8, 8)]
+    for key, (h, y) in outs.items():
+        assert torch.equal(h, h0), f"h, runs {key}"
+        assert torch.equal(y, y0), f"y, runs {key}"
+
+
 def test_block_boundaries():
     counts = {1: 1, 4: 16, 7: 17, 10: 40}
     slots = [e for e, c in counts.items() for _ in range(c)]
@@ -329,7 +349,7 @@ def test_the_library_refuses_a_launch_past_its_offset_range():
     buf = torch.zeros(64, dtype=torch.int64, device="cuda")
     huge = (0xF0000000 // (2 * QWEN[1])) // 16 + 1                 # h rows one block past
     rc = lib.vaayu_prefill_down(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
-                                0, buf.data_ptr(), 2, buf.data_ptr(), huge, g, 0, 0, 0,
+                                0, 8, buf.data_ptr(), 2, buf.data_ptr(), huge, g, 0, 0, 0,
                                 _lib.stream_ptr(buf.device))
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     tokens_over = (0xF0000000 // (2 * QWEN[0])) + 1                 # x rows one token past

@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -54,7 +54,8 @@ def _bind(lib):
         "vaayu_prefill_gate_up": (ctypes.c_int, [vp, vp, vp, vp, i32, vp, i32, i32, gp, i32,
                                                  i32, vp]),
         "vaayu_prefill_down": (ctypes.c_int,
-                               [vp, vp, vp, vp, i32, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
+                               [vp, vp, vp, vp, i32, i32, vp, i32, vp, i32, gp, i32, i32, i32,
+                                vp]),
         "vaayu_prefill_run_blocks": (ctypes.c_int32, [i32]),
         "vaayu_prefill_reduce": (ctypes.c_int, [vp, vp, vp, i32, i32, i32, vp]),
         "vaayu_dequant_blob": (ctypes.c_int, [vp, vp, i32, vp, i32, i64, i32, i32, vp]),
@@ -71,8 +72,8 @@ def _bind(lib):
         "vaayu_fused3d_gate_up": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32,
                                                  i32, i32, i32, vp, vp, ctypes.c_float,
                                                  ctypes.c_float, vp]),
-        "vaayu_fused3d_down": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
-                                              i32, i32, vp, vp, vp]),
+        "vaayu_fused3d_down": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, i32, vp, vp, i32, i32,
+                                              i32, i32, i32, vp, vp, vp]),
         "vaayu_router_logits": (ctypes.c_int, [vp, vp, i32, vp, i32, i32, i32, i32, vp]),
         "vaayu_decode_noalloc": (ctypes.c_int, [vp, vp, vp, i32, vp, i32, gp, i32, i32, i32,
                                                 vp]),

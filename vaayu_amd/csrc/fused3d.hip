@@ -170,16 +170,21 @@ fused3d_gate_up_kernel(Fused3DArgs p, const void* __restrict__ x, void* __restri
 #undef F3_GU
 }
 
+template <int R>
 __global__ void __launch_bounds__(64 * kWaves)
 fused3d_down_kernel(Fused3DArgs p, const void* __restrict__ h, const float* __restrict__ gammas,
                     float* __restrict__ y) {
-  __shared__ __align__(1024) char lds0[kRunDown * 16 * (2 * 512 / 4)];
-  __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / 4)];
-  __shared__ int rid_s[kRunDown * 16];
-  __shared__ float w_s[kRunDown * 16];
-  const Item it = item_here<kRunDown>(p.work, p.n_blocks, p.n_tiles);
+  __shared__ __align__(1024) char lds0[R * 16 * (2 * 512 / 4)];
+  __shared__ __align__(1024) char lds1[R * 16 * (2 * 512 / 4)];
+  __shared__ int rid_s[R * 16];
+  __shared__ float w_s[R * 16];
+  const Item it = item_here<R>(p.work, p.n_blocks, p.n_tiles);
 #define F3_DN(S_) oss_down_run<S_>(it, p, h, gammas, y, lds0, lds1, rid_s, w_s)
-  VAAYU_F3D_BY_S(F3_DN)
+  if constexpr (R > kRunDownShort) {
+    VAAYU_F3D_BY_S16(F3_DN)
+  } else {
+    VAAYU_F3D_BY_S(F3_DN)
+  }
 #undef F3_DN
 }
 
@@ -228,7 +233,7 @@ extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const i
 
 extern "C" int vaayu_fused3d_down(const void* h, const int64_t* rows, const int64_t* tbl,
                                   const int64_t* btbl, const int64_t* work, int32_t n_slots,
-                                  const float* gammas, float* y,
+                                  int32_t run_blocks, const float* gammas, float* y,
                                   int32_t n_blocks, int32_t top_k, int32_t hidden,
                                   int32_t inter, int32_t inter_pad, const void* codes_end,
                                   const void* scales_end, void* stream) {
@@ -236,6 +241,8 @@ extern "C" int vaayu_fused3d_down(const void* h, const int64_t* rows, const int6
   if (!h || !rows || !tbl || !btbl || !work || !gammas || !y || !codes_end || !scales_end)
     return set_error(-1, "null pointer argument");
   if (n_slots < 0 || n_slots > n_blocks) return set_error(-2, "n_slots must be in [0, n_blocks]");
+  if (run_blocks < 1 || run_blocks > kRunDown)
+    return set_error(-2, "run_blocks must be in [1, vaayu_prefill_run_blocks(1)]");
   if (int rc = fused3d_check(n_blocks, top_k, inter, inter_pad, hidden)) return rc;
   if (const char* why = rows_out_of_reach(n_blocks, 1, 0, 2ll * inter_pad))
     return set_error(-2, why);
@@ -248,6 +255,11 @@ extern "C" int vaayu_fused3d_down(const void* h, const int64_t* rows, const int6
   p.alpha = 0.f; p.limit = 0.f;
   if (n_slots == 0) return 0;
   const dim3 grid = work_grid(n_slots, p.n_tiles), block(64 * kWaves);
-  hipLaunchKernelGGL(fused3d_down_kernel, grid, block, 0, (hipStream_t)stream, p, h, gammas, y);
+  if (run_blocks <= kRunDownShort)
+    hipLaunchKernelGGL(fused3d_down_kernel<kRunDownShort>, grid, block, 0, (hipStream_t)stream, p,
+                       h, gammas, y);
+  else
+    hipLaunchKernelGGL(fused3d_down_kernel<kRunDown>, grid, block, 0, (hipStream_t)stream, p, h,
+                       gammas, y);
   return check_launch("fused-3D down");
 }

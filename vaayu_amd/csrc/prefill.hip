@@ -66,7 +66,7 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
   const PrefillArgs p{n_blocks, (g->inter + kTileN - 1) / kTileN, top_k, g->hidden, g->inter,
                       log2_of(g->group),
                       g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype,
-                      work, n_slots};
+                      work, n_slots, kRunGateUp};
   hipStream_t st = (hipStream_t)stream;
   if (g->format != VAAYU_FMT_INT) {
     const int rc = prefill_gate_up_formats(x, rows, table, h, p, g, act, st);
@@ -84,7 +84,7 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
 }
 
 extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int64_t* table,
-                                  const int64_t* work, int32_t n_slots,
+                                  const int64_t* work, int32_t n_slots, int32_t run_blocks,
                                   const void* routing_weights, int32_t rw_dtype, float* y,
                                   int32_t n_blocks, const vaayu_geom* g, int32_t act,
                                   int32_t scale_dtype, int32_t w_round, void* stream) {
@@ -93,6 +93,8 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
     return set_error(-1, "null pointer argument");
   if (n_blocks <= 0) return set_error(-1, "n_blocks must be positive");
   if (n_slots < 0 || n_slots > n_blocks) return set_error(-1, "n_slots must be in [0, n_blocks]");
+  if (run_blocks < 1 || run_blocks > kRunDown)
+    return set_error(-1, "run_blocks must be in [1, vaayu_prefill_run_blocks(1)]");
   if (scale_dtype < 0 || scale_dtype > 3 || rw_dtype < 0 || rw_dtype > 2)
     return set_error(-1, "scale / routing-weight dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
@@ -101,7 +103,7 @@ extern "C" int vaayu_prefill_down(const void* h, const int64_t* rows, const int6
   const PrefillArgs p{n_blocks, (g->hidden + kTileN - 1) / kTileN, 1, g->hidden, g->inter,
                       log2_of(g->group),
                       g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype,
-                      work, n_slots};
+                      work, n_slots, run_blocks};
   hipStream_t st = (hipStream_t)stream;
   if (g->format != VAAYU_FMT_INT) {
     const int rc = prefill_down_formats(h, rows, table, routing_weights, rw_dtype, y, p, g, act,

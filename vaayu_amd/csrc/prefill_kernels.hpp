@@ -63,7 +63,9 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // and the 16-block path's 128 accumulators fit two waves per SIMD.
 
 constexpr int kRunGateUp = 16;   // blocks per run, gate/up
-constexpr int kRunDown = 8;      // blocks per run, down
+constexpr int kRunDown = 16;     // blocks per run, down: the longest, and
+constexpr int kRunDownShort = 8; // the kernel of calls whose runs are at most this long
+                                 // (118 VGPRs, so two blocks share a CU)
 constexpr int kWaves = 8;        // waves per workgroup, 16 weight rows (N) each
 constexpr int kTileN = 16 * kWaves;
 
@@ -349,7 +351,7 @@ __device__ __forceinline__ void k_step_split(const char* cur,
 // A pair tile holds two steps of S*16 rows, inside the kernels' tiles of one step of a
 // full run (kRunGateUp or kRunDown blocks): S <= half a run.
 constexpr int kPairS = 4;
-static_assert(2 * kPairS <= kRunGateUp && 2 * kPairS <= kRunDown,
+static_assert(2 * kPairS <= kRunGateUp && 2 * kPairS <= kRunDownShort,
               "a pair of steps must fit one LDS tile");
 
 template <int F, int ACT, int SW, int NR, int S>
@@ -414,7 +416,7 @@ __device__ __forceinline__ void run_k_pairs(const Role (&role)[NR], rsrc_t src,
   constexpr int CPU = 128 / BITS;
   constexpr int KS = 4 * CPU;
   using A = AStage<KS, S>;
-  static_assert(2 * S <= kRunGateUp && 2 * S <= kRunDown, "a pair of steps must fit one tile");
+  static_assert(2 * S <= kRunGateUp && 2 * S <= kRunDownShort, "a pair of steps must fit one tile");
   const Masks M = make_masks();
   const int T = K / KS, last = K - KS;
   BStep c0[NR], c1[NR], n0[NR], n1[NR];
@@ -661,7 +663,7 @@ prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ r
 #undef GU_CALL
 }
 
-template <int F, int ACT, int SW>
+template <int F, int ACT, int SW, int R>
 __global__ void __launch_bounds__(64 * kWaves)
 prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows,
                     const int64_t* __restrict__ tbl, const int64_t* __restrict__ work,
@@ -670,15 +672,19 @@ prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows
                     int gshift, int rshift, int sc_dt, int64_t down_w, int64_t down_s,
                     int w_round) {
   constexpr int BITS = CodeBits<F>::value;
-  __shared__ __align__(1024) char lds0[kRunDown * 16 * (2 * 512 / BITS)];
-  __shared__ __align__(1024) char lds1[kRunDown * 16 * (2 * 512 / BITS)];
-  const Item it = item_here<kRunDown>(work, n_blocks, n_tiles);
-  __shared__ int rid_s[kRunDown * 16];
-  __shared__ float w_s[kRunDown * 16];
+  __shared__ __align__(1024) char lds0[R * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds1[R * 16 * (2 * 512 / BITS)];
+  const Item it = item_here<R>(work, n_blocks, n_tiles);
+  __shared__ int rid_s[R * 16];
+  __shared__ float w_s[R * 16];
 #define DN_CALL(S_) down_run<F, ACT, SW, S_>(it, h, rows, tbl, rw, rw_dt, y, hidden, inter, gshift, \
                                          rshift, sc_dt, down_w, down_s, w_round, lds0, lds1, \
                                          rid_s, w_s)
-  VAAYU_BY_S8(DN_CALL)
+  if constexpr (R > kRunDownShort) {
+    VAAYU_BY_S16(DN_CALL)
+  } else {
+    VAAYU_BY_S8(DN_CALL)
+  }
 #undef DN_CALL
 }
 
@@ -697,8 +703,9 @@ inline int log2_of(int v) {
 
 struct PrefillArgs {
   int n_blocks, n_tiles, top_k, hidden, inter, gshift, rshift, sc_dt;
-  const int64_t* work;    // the work list (see item_here) and its slots per XCD
-  int n_slots;
+  const int64_t* work;    // the work list (see item_here), its slots per XCD and its
+  int n_slots;            // longest run (blocks)
+  int run;
 };
 
 // Workgroups of a launch over n_slots slots of n_tiles N tiles each.
@@ -723,9 +730,14 @@ void launch_prefill_down(const void* h, const int64_t* rows, const int64_t* tbl,
                          int w_round, hipStream_t st) {
   const dim3 grid = work_grid(p.n_slots, p.n_tiles), block(64 * kWaves);
   if (p.n_slots == 0) return;
-  hipLaunchKernelGGL((prefill_down_kernel<F, ACT, SW>), grid, block, 0, st, h, rows, tbl, p.work, rw,
-                     rw_dt, y, p.n_blocks, p.n_tiles, p.hidden, p.inter, p.gshift, p.rshift,
-                     p.sc_dt, g->down_w, g->down_s, w_round);
+  if (p.run <= kRunDownShort)
+    hipLaunchKernelGGL((prefill_down_kernel<F, ACT, SW, kRunDownShort>), grid, block, 0, st, h,
+                       rows, tbl, p.work, rw, rw_dt, y, p.n_blocks, p.n_tiles, p.hidden, p.inter,
+                       p.gshift, p.rshift, p.sc_dt, g->down_w, g->down_s, w_round);
+  else
+    hipLaunchKernelGGL((prefill_down_kernel<F, ACT, SW, kRunDown>), grid, block, 0, st, h, rows,
+                       tbl, p.work, rw, rw_dt, y, p.n_blocks, p.n_tiles, p.hidden, p.inter,
+                       p.gshift, p.rshift, p.sc_dt, g->down_w, g->down_s, w_round);
 }
 
 // e4m3 / e2m1 launches (prefill_formats.hip): 0, or a negative code with the error set.

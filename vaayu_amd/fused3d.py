@@ -120,15 +120,15 @@ class Fused3DExperts:
         n_cus = pk._cu_count(self.device)
         w_gu, s_gu = pk._prefill_work(nblk[lay].tolist(), pk._run_blocks(0),
                                       -(-self.I // 128), n_cus)
-        w_dn, s_dn = pk._prefill_work(nblk[lay].tolist(), pk._run_blocks(1),
-                                      -(-self.H // 128), n_cus)
+        r_dn = pk._down_run(nblk[lay].tolist(), -(-self.H // 128), n_cus)
+        w_dn, s_dn = pk._prefill_work(nblk[lay].tolist(), r_dn)
         parts = cols + [slot_order, w_gu, w_dn]
         dev = pk._PF_TABLES.put(torch.cat(parts), self.device)
         out, at = [], 0
         for t in parts:
             out.append(dev[at:at + t.numel()])
             at += t.numel()
-        work = pk.PrefillWork(out[-2], s_gu, out[-1], s_dn)
+        work = pk.PrefillWork(out[-2], s_gu, out[-1], s_dn, r_dn)
         return (*out[:-2], n_blocks, work)
 
     def forward(self, x, expert_ids, routing_weights):
@@ -183,7 +183,7 @@ class Fused3DExperts:
         _lib.check(rc, "vaayu_fused3d_gate_up")
         rc = lib.vaayu_fused3d_down(
             h.data_ptr(), rows.data_ptr(), dn_t.data_ptr(), dn_b.data_ptr(),
-            work.down.data_ptr(), work.down_slots, gammas.data_ptr(),
+            work.down.data_ptr(), work.down_slots, work.down_run, gammas.data_ptr(),
             y.data_ptr(), n_blocks, top_k, self.H, self.I, self.Ip, self._end(self.dn_codes),
             self._end(self.dn_scales), st)
         _lib.check(rc, "vaayu_fused3d_down")

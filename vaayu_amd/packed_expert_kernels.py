@@ -680,16 +680,17 @@ def _run_cost(blocks: int) -> float:
 
 
 class PrefillWork(NamedTuple):
-    """The work lists of one call's grouped launches (int64 on the device, `_prefill_work`)
-    and their slots per XCD."""
+    """The work lists of one call's grouped launches (int64 on the device, `_prefill_work`),
+    their slots per XCD, and the longest run of the down list."""
     gate_up: torch.Tensor
     gate_up_slots: int
     down: torch.Tensor
     down_slots: int
+    down_run: int
 
     def clone(self) -> "PrefillWork":
         return PrefillWork(self.gate_up.clone(), self.gate_up_slots, self.down.clone(),
-                           self.down_slots)
+                           self.down_slots, self.down_run)
 
 
 _RUN_BLOCKS = {}
@@ -728,6 +729,18 @@ def _run_length(blocks, run: int, n_tiles: int, n_cus: int) -> int:
             best, best_t = r, t
         r //= 2
     return best
+
+
+def _down_run(blocks, n_tiles: int, n_cus: int) -> int:
+    """The down launch's run length. The library's down kernel for runs of up to 16 blocks
+    holds twice the accumulators of the one for runs of up to 8 (210 VGPRs against 118), so
+    one workgroup runs per CU instead of two: it pays where the longer runs halve the run
+    count (Mixtral's 512-token layer, experts of 8-9 blocks: down 213 -> 175 us) and not
+    where they save little (DeepSeek-V3's Zipf routing: 11 % fewer runs, 1047 -> 1138 us)."""
+    longest = _run_blocks(1)
+    runs = {r: sum(-(-int(b) // r) for b in blocks) for r in (8, longest)}
+    run = longest if runs[longest] <= 0.75 * runs[8] else 8
+    return min(_run_length(blocks, run, n_tiles, n_cus), max(int(b) for b in blocks))
 
 
 def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
@@ -803,15 +816,17 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     lay_geom = _layout(blobs[int(live[0])]["geom"])
     hidden, inter = lay_geom["gate"][3], lay_geom["gate"][2]
     n_cus = _cu_count(device)
-    w_gu, s_gu = _prefill_work(blocks[lay].tolist(), _run_blocks(0), -(-inter // 128), n_cus)
-    w_dn, s_dn = _prefill_work(blocks[lay].tolist(), _run_blocks(1), -(-hidden // 128), n_cus)
+    blk = blocks[lay].tolist()
+    w_gu, s_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
+    r_dn = _down_run(blk, -(-hidden // 128), n_cus)
+    w_dn, s_dn = _prefill_work(blk, r_dn)
     parts = [tbl, rows, ord_, w_gu, w_dn]
     dev = _PF_TABLES.put(torch.cat(parts), device)
     at = [0]
     for t in parts:
         at.append(at[-1] + t.numel())
     sl = [dev[at[i]:at[i + 1]] for i in range(len(parts))]
-    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn)
+    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn, r_dn)
 
 
 def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
@@ -838,7 +853,8 @@ def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None, *, work):
     if y is None:
         y = torch.empty(h.shape[0], g.hidden, dtype=torch.float32, device=h.device)
     _lib.check(lib.vaayu_prefill_down(h.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
-                                      work.down.data_ptr(), work.down_slots, rw.data_ptr(), _DTYPE_CODE[rw.dtype], y.data_ptr(),
+                                      work.down.data_ptr(), work.down_slots, work.down_run,
+                                      rw.data_ptr(), _DTYPE_CODE[rw.dtype], y.data_ptr(),
                                       n_blocks, g, _DTYPE_CODE[h.dtype], sc,
                                       int(_rounds_weighted(rw.dtype, h.dtype)),
                                       _lib.stream_ptr(h.device)),
