@@ -84,3 +84,17 @@ def test_work_lists_spread_the_work_over_the_xcds():
             for x, _first, n in _runs(pk._prefill_work(blocks, run)[0]):
                 load[x] += pk._run_cost(n)
             assert load.max() / load.mean() < 1.05, (seed, run, load)
+
+
+def test_run_lengths_chosen_per_call():
+    """Gate/up: one long expert is cut into runs of 8, so its 2048 rows fill the 256 CUs,
+    while a Zipf-routed call keeps runs of 16. Down: the kernel for runs of up to 16 blocks
+    only where it halves the runs (experts of 8-9 blocks), not for Zipf routing."""
+    assert pk._run_length([128], 16, 16, 256) == 8
+    eidx = _zipf(2048, 256, 8, 0)
+    blocks = ((pk._prefill_plan(eidx)[2] + 15) // 16).tolist()
+    assert pk._run_length(blocks, 16, 16, 256) == 16
+    assert pk._down_run(blocks, 56, 256) == 8
+    mixtral = [9, 9, 8, 9, 8, 8, 9, 8]
+    assert pk._down_run(mixtral, 32, 256) == 9
+    assert pk._down_run([1, 2, 1, 3], 16, 256) <= 3
