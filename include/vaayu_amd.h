@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define VAAYU_ABI_VERSION 11
+#define VAAYU_ABI_VERSION 12
 
 enum { VAAYU_BF16 = 0, VAAYU_FP16 = 1, VAAYU_FP32 = 2 };
 
@@ -91,12 +91,16 @@ int vaayu_decode_down(const void *h, const int64_t *table, const void *routing_w
  *       vaayu_prefill_run_blocks(0) gives), or -1; each run is computed for every N tile on
  *       XCD x. Every block of the table must lie in exactly one run; an entry that does
  *       not fit the table computes nothing. n_slots in [0, n_blocks].
+ * run_blocks  the longest run in `work` (calls whose runs are at most 4 blocks long take a
+ *       kernel that fits two workgroups per CU); an entry longer than run_blocks computes
+ *       nothing.
  * h     [tokens * top_k, inter] (dtype `act`); padding rows are never written
  * x and h rows are addressed with 32-bit byte offsets: a launch whose tables could hold
  * rows past 0xF0000000 bytes (n_blocks * 16 / top_k tokens of x) is refused with -2; split
  * such a call into token chunks (every row's arithmetic is independent of its launch-mates). */
 int vaayu_prefill_gate_up(const void *x, const int64_t *rows, const int64_t *table,
-                          const int64_t *work, int32_t n_slots, void *h, int32_t n_blocks,
+                          const int64_t *work, int32_t n_slots, int32_t run_blocks, void *h,
+                          int32_t n_blocks,
                           int32_t top_k, const vaayu_geom *geom, int32_t act,
                           int32_t scale_dtype, void *stream);
 
@@ -253,7 +257,7 @@ int vaayu_gdn_gated_norm(const void *x, const void *z, const void *w, void *o,
  * h = fma(s, up, s). x [tokens, hidden_pad] bf16. */
 int vaayu_fused3d_gate_up(const void *x, const int64_t *rows, const int64_t *tbl,
                           const int64_t *btbl, const int64_t *work, int32_t n_slots,
-                          void *h, int32_t n_blocks, int32_t top_k,
+                          int32_t run_blocks, void *h, int32_t n_blocks, int32_t top_k,
                           int32_t hidden, int32_t hidden_pad, int32_t inter, int32_t inter_pad,
                           const void *codes_end, const void *scales_end, float alpha,
                           float limit, void *stream);

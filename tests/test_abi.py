@@ -43,10 +43,10 @@ def test_bad_arguments_are_rejected_without_a_launch():
     bad = _lib.geom_struct((3, 32, (("gate", 512, 2048), ("down", 2048, 512), ("up", 512, 2048))))
     rc = lib.vaayu_decode_gate_up(256, 256, 256, 1, ctypes.byref(bad), 0, 0, None)
     assert rc == -2 and b"bit width" in lib.vaayu_last_error()
-    rc = lib.vaayu_prefill_gate_up(1, 1, 1, 1, 0, 1, 1, 1, ctypes.byref(g), 2, 0, None)
+    rc = lib.vaayu_prefill_gate_up(1, 1, 1, 1, 0, 1, 1, 1, 1, ctypes.byref(g), 2, 0, None)
     assert rc == -2 and b"activation" in lib.vaayu_last_error()
     small = _lib.geom_struct((4, 32, (("gate", 64, 64), ("down", 64, 64), ("up", 64, 64))))
-    rc = lib.vaayu_prefill_gate_up(1, 1, 1, 1, 0, 1, 1, 1, ctypes.byref(small), 0, 0, None)
+    rc = lib.vaayu_prefill_gate_up(1, 1, 1, 1, 0, 1, 1, 1, 1, ctypes.byref(small), 0, 0, None)
     assert rc == -2 and b"K tile" in lib.vaayu_last_error()
     rc = lib.vaayu_dequant_blob(1, 1, 0, 1, 0, 0, 4, 32, None)
     assert rc == -1

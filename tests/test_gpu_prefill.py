@@ -354,7 +354,7 @@ def test_the_library_refuses_a_launch_past_its_offset_range():
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     tokens_over = (0xF0000000 // (2 * QWEN[0])) + 1                 # x rows one token past
     rc = lib.vaayu_prefill_gate_up(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
-                                   buf.data_ptr(), 0, buf.data_ptr(), -(-tokens_over // 16), 1,
+                                   buf.data_ptr(), 0, 16, buf.data_ptr(), -(-tokens_over // 16), 1,
                                    g, 0, 0, _lib.stream_ptr(buf.device))
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     torch.cuda.synchronize()

@@ -56,7 +56,8 @@ def test_work_lists_cover_every_block_once_in_runs_of_one_expert():
                                generator=g).tolist()
         starts = np.cumsum([0] + blocks)
         for run in (8, 16):
-            work, n_slots = pk._prefill_work(blocks, run)
+            work, n_slots, longest = pk._prefill_work(blocks, run)
+            assert longest == min(run, max(blocks))
             assert work.dtype == torch.int64 and work.numel() == n_slots * 8
             runs = _runs(work)
             n_runs = sum(-(-b // run) for b in blocks)

@@ -10,7 +10,7 @@ import torch  # noqa: F401  -- loads the HIP runtime the library binds to
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvaayu_amd.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # The reference's `_DTYPE_CODE` (vaayu/packed_expert_kernels.py:70).
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -51,8 +51,8 @@ def _bind(lib):
         "vaayu_last_error": (ctypes.c_char_p, []),
         "vaayu_decode_gate_up": (ctypes.c_int, [vp, vp, vp, i32, gp, i32, i32, vp]),
         "vaayu_decode_down": (ctypes.c_int, [vp, vp, vp, i32, vp, i32, gp, i32, i32, i32, vp]),
-        "vaayu_prefill_gate_up": (ctypes.c_int, [vp, vp, vp, vp, i32, vp, i32, i32, gp, i32,
-                                                 i32, vp]),
+        "vaayu_prefill_gate_up": (ctypes.c_int, [vp, vp, vp, vp, i32, i32, vp, i32, i32, gp,
+                                                 i32, i32, vp]),
         "vaayu_prefill_down": (ctypes.c_int,
                                [vp, vp, vp, vp, i32, i32, vp, i32, vp, i32, gp, i32, i32, i32,
                                 vp]),
@@ -69,8 +69,8 @@ def _bind(lib):
                                                  i32, i32, i32, vp]),
         "vaayu_gdn_gated_norm": (ctypes.c_int, [vp, vp, vp, vp, vp, i64, i32, ctypes.c_float,
                                                 i32, i32, i32, i32, vp]),
-        "vaayu_fused3d_gate_up": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32,
-                                                 i32, i32, i32, vp, vp, ctypes.c_float,
+        "vaayu_fused3d_gate_up": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, i32, vp, i32, i32,
+                                                 i32, i32, i32, i32, vp, vp, ctypes.c_float,
                                                  ctypes.c_float, vp]),
         "vaayu_fused3d_down": (ctypes.c_int, [vp, vp, vp, vp, vp, i32, i32, vp, vp, i32, i32,
                                               i32, i32, i32, vp, vp, vp]),

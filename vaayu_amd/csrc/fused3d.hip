@@ -159,14 +159,22 @@ __device__ __forceinline__ void oss_down_run(const Item& it, const Fused3DArgs& 
     case 16: CALL(16); break; default: break;                                       \
   }
 
+template <int R>
 __global__ void __launch_bounds__(64 * kWaves)
 fused3d_gate_up_kernel(Fused3DArgs p, const void* __restrict__ x, void* __restrict__ h) {
-  __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / 4)];
-  __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / 4)];
-  __shared__ int rid_s[kRunGateUp * 16];
-  const Item it = item_here<kRunGateUp>(p.work, p.n_blocks, p.n_tiles);
+  __shared__ __align__(1024) char lds0[tile_blocks(R) * 16 * (2 * 512 / 4)];
+  __shared__ __align__(1024) char lds1[tile_blocks(R) * 16 * (2 * 512 / 4)];
+  __shared__ int rid_s[R * 16];
+  const Item it = item_here<R>(p.work, p.n_blocks, p.n_tiles);
 #define F3_GU(S_) oss_gate_up_run<S_>(it, p, x, h, lds0, lds1, rid_s)
-  VAAYU_F3D_BY_S16(F3_GU)
+  if constexpr (R > kRunGateUpShort) {
+    VAAYU_F3D_BY_S16(F3_GU)
+  } else {
+    switch (it.S) {
+      case 1: F3_GU(1); break; case 2: F3_GU(2); break; case 3: F3_GU(3); break;
+      case 4: F3_GU(4); break; default: break;
+    }
+  }
 #undef F3_GU
 }
 
@@ -174,8 +182,8 @@ template <int R>
 __global__ void __launch_bounds__(64 * kWaves)
 fused3d_down_kernel(Fused3DArgs p, const void* __restrict__ h, const float* __restrict__ gammas,
                     float* __restrict__ y) {
-  __shared__ __align__(1024) char lds0[R * 16 * (2 * 512 / 4)];
-  __shared__ __align__(1024) char lds1[R * 16 * (2 * 512 / 4)];
+  __shared__ __align__(1024) char lds0[tile_blocks(R) * 16 * (2 * 512 / 4)];
+  __shared__ __align__(1024) char lds1[tile_blocks(R) * 16 * (2 * 512 / 4)];
   __shared__ int rid_s[R * 16];
   __shared__ float w_s[R * 16];
   const Item it = item_here<R>(p.work, p.n_blocks, p.n_tiles);
@@ -205,7 +213,7 @@ static int fused3d_check(int n_blocks, int top_k, int k, int k_pad, int n_out) {
 
 extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const int64_t* tbl,
                                      const int64_t* btbl, const int64_t* work, int32_t n_slots,
-                                     void* h, int32_t n_blocks,
+                                     int32_t run_blocks, void* h, int32_t n_blocks,
                                      int32_t top_k, int32_t hidden, int32_t hidden_pad,
                                      int32_t inter, int32_t inter_pad, const void* codes_end,
                                      const void* scales_end, float alpha, float limit,
@@ -214,6 +222,8 @@ extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const i
   if (!x || !rows || !tbl || !btbl || !work || !h || !codes_end || !scales_end)
     return set_error(-1, "null pointer argument");
   if (n_slots < 0 || n_slots > n_blocks) return set_error(-2, "n_slots must be in [0, n_blocks]");
+  if (run_blocks < 1 || run_blocks > kRunGateUp)
+    return set_error(-2, "run_blocks must be in [1, vaayu_prefill_run_blocks(0)]");
   if (int rc = fused3d_check(n_blocks, top_k, hidden, hidden_pad, inter)) return rc;
   if (inter_pad < inter) return set_error(-2, "h's row pitch is below the intermediate size");
   if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * hidden_pad, 0))
@@ -227,7 +237,12 @@ extern "C" int vaayu_fused3d_gate_up(const void* x, const int64_t* rows, const i
   p.alpha = alpha; p.limit = limit;
   if (n_slots == 0) return 0;
   const dim3 grid = work_grid(n_slots, p.n_tiles), block(64 * kWaves);
-  hipLaunchKernelGGL(fused3d_gate_up_kernel, grid, block, 0, (hipStream_t)stream, p, x, h);
+  if (run_blocks <= kRunGateUpShort)
+    hipLaunchKernelGGL(fused3d_gate_up_kernel<kRunGateUpShort>, grid, block, 0,
+                       (hipStream_t)stream, p, x, h);
+  else
+    hipLaunchKernelGGL(fused3d_gate_up_kernel<kRunGateUp>, grid, block, 0, (hipStream_t)stream, p,
+                       x, h);
   return check_launch("fused-3D gate/up");
 }
 

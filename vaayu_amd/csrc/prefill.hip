@@ -52,13 +52,16 @@ const char* prefill_unsupported(const vaayu_geom* g, int act, int sc) {
 using namespace vaayu;
 
 extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const int64_t* table,
-                                     const int64_t* work, int32_t n_slots, void* h,
+                                     const int64_t* work, int32_t n_slots, int32_t run_blocks,
+                                     void* h,
                                      int32_t n_blocks, int32_t top_k, const vaayu_geom* g,
                                      int32_t act, int32_t scale_dtype, void* stream) {
   clear_error();
   if (!x || !rows || !table || !work || !h || !g) return set_error(-1, "null pointer argument");
   if (n_blocks <= 0 || top_k <= 0) return set_error(-1, "n_blocks / top_k must be positive");
   if (n_slots < 0 || n_slots > n_blocks) return set_error(-1, "n_slots must be in [0, n_blocks]");
+  if (run_blocks < 1 || run_blocks > kRunGateUp)
+    return set_error(-1, "run_blocks must be in [1, vaayu_prefill_run_blocks(0)]");
   if (scale_dtype < 0 || scale_dtype > 3) return set_error(-1, "scale dtype");
   if (const char* why = prefill_unsupported(g, act, scale_dtype)) return set_error(-2, why);
   if (const char* why = rows_out_of_reach(n_blocks, top_k, 2ll * g->hidden, 0))
@@ -66,7 +69,7 @@ extern "C" int vaayu_prefill_gate_up(const void* x, const int64_t* rows, const i
   const PrefillArgs p{n_blocks, (g->inter + kTileN - 1) / kTileN, top_k, g->hidden, g->inter,
                       log2_of(g->group),
                       g->format == VAAYU_FMT_E4M3 ? log2_of(g->block_rows) : 0, scale_dtype,
-                      work, n_slots, kRunGateUp};
+                      work, n_slots, run_blocks};
   hipStream_t st = (hipStream_t)stream;
   if (g->format != VAAYU_FMT_INT) {
     const int rc = prefill_gate_up_formats(x, rows, table, h, p, g, act, st);

@@ -62,7 +62,9 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // dequant of the next step's operands, so the two steps' operands are never live together
 // and the 16-block path's 128 accumulators fit two waves per SIMD.
 
-constexpr int kRunGateUp = 16;   // blocks per run, gate/up
+constexpr int kRunGateUp = 16;   // blocks per run, gate/up: the longest, and
+constexpr int kRunGateUpShort = 4;  // the kernel of calls whose runs are at most this long
+                                    // (128 VGPRs, so two blocks share a CU)
 constexpr int kRunDown = 16;     // blocks per run, down: the longest, and
 constexpr int kRunDownShort = 8; // the kernel of calls whose runs are at most this long
                                  // (118 VGPRs, so two blocks share a CU)
@@ -351,6 +353,10 @@ __device__ __forceinline__ void k_step_split(const char* cur,
 // A pair tile holds two steps of S*16 rows, inside the kernels' tiles of one step of a
 // full run (kRunGateUp or kRunDown blocks): S <= half a run.
 constexpr int kPairS = 4;
+
+// Blocks of rows an LDS tile of a kernel for runs of up to R blocks holds: one step of a
+// full run, and for runs short enough to take pairs, two steps of the longest such run.
+constexpr int tile_blocks(int R) { return R <= kPairS ? 2 * R : R; }
 static_assert(2 * kPairS <= kRunGateUp && 2 * kPairS <= kRunDownShort,
               "a pair of steps must fit one LDS tile");
 
@@ -644,7 +650,7 @@ __device__ __forceinline__ void down_run(const Item& it, const void* h, const in
     case 16: CALL(16); break; default: break;                                       \
   }
 
-template <int F, int ACT, int SW>
+template <int F, int ACT, int SW, int R>
 __global__ void __launch_bounds__(64 * kWaves)
 prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ rows,
                        const int64_t* __restrict__ tbl, const int64_t* __restrict__ work,
@@ -652,14 +658,18 @@ prefill_gate_up_kernel(const void* __restrict__ x, const int64_t* __restrict__ r
                        int n_tiles, int top_k, int hidden, int inter, int gshift, int rshift,
                        int sc_dt, int64_t gate_w, int64_t gate_s, int64_t up_w, int64_t up_s) {
   constexpr int BITS = CodeBits<F>::value;
-  __shared__ __align__(1024) char lds0[kRunGateUp * 16 * (2 * 512 / BITS)];
-  __shared__ __align__(1024) char lds1[kRunGateUp * 16 * (2 * 512 / BITS)];
-  const Item it = item_here<kRunGateUp>(work, n_blocks, n_tiles);
-  __shared__ int rid_s[kRunGateUp * 16];
+  __shared__ __align__(1024) char lds0[tile_blocks(R) * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds1[tile_blocks(R) * 16 * (2 * 512 / BITS)];
+  const Item it = item_here<R>(work, n_blocks, n_tiles);
+  __shared__ int rid_s[R * 16];
 #define GU_CALL(S_) gate_up_run<F, ACT, SW, S_>(it, x, rows, tbl, h, top_k, hidden, inter, gshift, \
                                             rshift, sc_dt, gate_w, gate_s, up_w, up_s, lds0, lds1, \
                                             rid_s)
-  VAAYU_BY_S16(GU_CALL)
+  if constexpr (R > kRunGateUpShort) {
+    VAAYU_BY_S16(GU_CALL)
+  } else {
+    VAAYU_BY_S4(GU_CALL)
+  }
 #undef GU_CALL
 }
 
@@ -672,8 +682,8 @@ prefill_down_kernel(const void* __restrict__ h, const int64_t* __restrict__ rows
                     int gshift, int rshift, int sc_dt, int64_t down_w, int64_t down_s,
                     int w_round) {
   constexpr int BITS = CodeBits<F>::value;
-  __shared__ __align__(1024) char lds0[R * 16 * (2 * 512 / BITS)];
-  __shared__ __align__(1024) char lds1[R * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds0[tile_blocks(R) * 16 * (2 * 512 / BITS)];
+  __shared__ __align__(1024) char lds1[tile_blocks(R) * 16 * (2 * 512 / BITS)];
   const Item it = item_here<R>(work, n_blocks, n_tiles);
   __shared__ int rid_s[R * 16];
   __shared__ float w_s[R * 16];
@@ -718,10 +728,14 @@ void launch_prefill_gate_up(const void* x, const int64_t* rows, const int64_t* t
                             const PrefillArgs& p, const vaayu_geom* g, hipStream_t st) {
   const dim3 grid = work_grid(p.n_slots, p.n_tiles), block(64 * kWaves);
   if (p.n_slots == 0) return;
-  hipLaunchKernelGGL((prefill_gate_up_kernel<F, ACT, SW>), grid, block, 0, st, x, rows, tbl,
-                     p.work, h,
-                     p.n_blocks, p.n_tiles, p.top_k, p.hidden, p.inter, p.gshift, p.rshift,
-                     p.sc_dt, g->gate_w, g->gate_s, g->up_w, g->up_s);
+  if (p.run <= kRunGateUpShort)
+    hipLaunchKernelGGL((prefill_gate_up_kernel<F, ACT, SW, kRunGateUpShort>), grid, block, 0, st,
+                       x, rows, tbl, p.work, h, p.n_blocks, p.n_tiles, p.top_k, p.hidden, p.inter,
+                       p.gshift, p.rshift, p.sc_dt, g->gate_w, g->gate_s, g->up_w, g->up_s);
+  else
+    hipLaunchKernelGGL((prefill_gate_up_kernel<F, ACT, SW, kRunGateUp>), grid, block, 0, st, x,
+                       rows, tbl, p.work, h, p.n_blocks, p.n_tiles, p.top_k, p.hidden, p.inter,
+                       p.gshift, p.rshift, p.sc_dt, g->gate_w, g->gate_s, g->up_w, g->up_s);
 }
 
 template <int F, int ACT, int SW>

@@ -118,17 +118,16 @@ class Fused3DExperts:
         slot_order = (torch.argsort(eidx, dim=1, stable=True)
                       + (torch.arange(n) * top_k)[:, None]).reshape(-1)
         n_cus = pk._cu_count(self.device)
-        w_gu, s_gu = pk._prefill_work(nblk[lay].tolist(), pk._run_blocks(0),
-                                      -(-self.I // 128), n_cus)
-        r_dn = pk._down_run(nblk[lay].tolist(), -(-self.H // 128), n_cus)
-        w_dn, s_dn = pk._prefill_work(nblk[lay].tolist(), r_dn)
+        blk = nblk[lay].tolist()
+        w_gu, s_gu, r_gu = pk._prefill_work(blk, pk._run_blocks(0), -(-self.I // 128), n_cus)
+        w_dn, s_dn, r_dn = pk._prefill_work(blk, pk._down_run(blk, -(-self.H // 128), n_cus))
         parts = cols + [slot_order, w_gu, w_dn]
         dev = pk._PF_TABLES.put(torch.cat(parts), self.device)
         out, at = [], 0
         for t in parts:
             out.append(dev[at:at + t.numel()])
             at += t.numel()
-        work = pk.PrefillWork(out[-2], s_gu, out[-1], s_dn, r_dn)
+        work = pk.PrefillWork(out[-2], s_gu, out[-1], s_dn, r_dn, r_gu)
         return (*out[:-2], n_blocks, work)
 
     def forward(self, x, expert_ids, routing_weights):
@@ -177,7 +176,7 @@ class Fused3DExperts:
         st = _lib.stream_ptr(xp.device)
         rc = lib.vaayu_fused3d_gate_up(
             xp.data_ptr(), rows.data_ptr(), gu_t.data_ptr(), gu_b.data_ptr(),
-            work.gate_up.data_ptr(), work.gate_up_slots, h.data_ptr(),
+            work.gate_up.data_ptr(), work.gate_up_slots, work.gate_up_run, h.data_ptr(),
             n_blocks, top_k, self.H, self.Hp, self.I, self.Ip, self._end(self.gu_codes),
             self._end(self.gu_scales), self.alpha, self.limit, st)
         _lib.check(rc, "vaayu_fused3d_gate_up")

@@ -681,16 +681,16 @@ def _run_cost(blocks: int) -> float:
 
 class PrefillWork(NamedTuple):
     """The work lists of one call's grouped launches (int64 on the device, `_prefill_work`),
-    their slots per XCD, and the longest run of the down list."""
+    their slots per XCD, and the longest run of each."""
     gate_up: torch.Tensor
     gate_up_slots: int
     down: torch.Tensor
     down_slots: int
     down_run: int
+    gate_up_run: int
 
     def clone(self) -> "PrefillWork":
-        return PrefillWork(self.gate_up.clone(), self.gate_up_slots, self.down.clone(),
-                           self.down_slots, self.down_run)
+        return self._replace(gate_up=self.gate_up.clone(), down=self.down.clone())
 
 
 _RUN_BLOCKS = {}
@@ -744,7 +744,7 @@ def _down_run(blocks, n_tiles: int, n_cus: int) -> int:
 
 
 def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
-    """(work, n_slots): the work list of one grouped launch over tables whose experts hold
+    """(work, n_slots, run): the work list of one grouped launch over tables whose experts hold
     `blocks` 16-row blocks each, in table order. Each expert's blocks form runs of up to
     `run` blocks (or the `_run_length` for `n_tiles` N tiles on `n_cus` CUs, when given)
     from its first block on; a run is one work item per N tile, all on one XCD (so they
@@ -752,10 +752,11 @@ def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
     first, each to the XCD with the least work so far (`_run_cost`) among those holding
     fewer than ceil(runs / 8), and each XCD takes its runs in that order.
     work[k * 8 + x] = first_block * 32 + length of XCD x's k-th run, or -1; n_slots is the
-    most runs an XCD holds. A row's arithmetic does not depend on its run's place or
-    length, so every choice gives the same bits."""
+    most runs an XCD holds, run the longest run. A row's arithmetic does not depend on its
+    run's place or length, so every choice gives the same bits."""
     if n_tiles and n_cus:
         run = _run_length(blocks, run, n_tiles, n_cus)
+    run = min(run, max((int(b) for b in blocks), default=1))
     runs, pos = [], 0
     for b in blocks:
         b = int(b)
@@ -772,7 +773,7 @@ def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
     for x, entries in enumerate(per):
         if entries:
             work[:len(entries), x] = torch.tensor(entries, dtype=torch.int64)
-    return work.reshape(-1), cap
+    return work.reshape(-1), cap, run
 
 
 def _prefill_layout(plan):
@@ -817,16 +818,15 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     hidden, inter = lay_geom["gate"][3], lay_geom["gate"][2]
     n_cus = _cu_count(device)
     blk = blocks[lay].tolist()
-    w_gu, s_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
-    r_dn = _down_run(blk, -(-hidden // 128), n_cus)
-    w_dn, s_dn = _prefill_work(blk, r_dn)
+    w_gu, s_gu, r_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
+    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus))
     parts = [tbl, rows, ord_, w_gu, w_dn]
     dev = _PF_TABLES.put(torch.cat(parts), device)
     at = [0]
     for t in parts:
         at.append(at[-1] + t.numel())
     sl = [dev[at[i]:at[i + 1]] for i in range(len(parts))]
-    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn, r_dn)
+    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn, r_dn, r_gu)
 
 
 def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
@@ -838,7 +838,7 @@ def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
         h = torch.empty(x.shape[0] * top_k, g.inter, dtype=x.dtype, device=x.device)
     _lib.check(lib.vaayu_prefill_gate_up(x.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
                                          work.gate_up.data_ptr(), work.gate_up_slots,
-                                         h.data_ptr(), n_blocks, top_k, g,
+                                         work.gate_up_run, h.data_ptr(), n_blocks, top_k, g,
                                          _DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device)),
                "vaayu_prefill_gate_up")
     return h
