@@ -350,14 +350,13 @@ __device__ __forceinline__ void k_step_split(const char* cur,
 // stay in flight until the next pair's barrier, so they have two steps to arrive, and half
 // as many barriers stand in a short run's K loop. Every output takes the same MFMAs in the
 // same order as in run_k, so the bits are the same whatever the run's length.
-// A pair tile holds two steps of S*16 rows, inside the kernels' tiles of one step of a
-// full run (kRunGateUp or kRunDown blocks): S <= half a run.
+// A pair tile holds two steps of S*16 rows (S <= kPairS), inside a kernel's LDS tile
+// (tile_blocks: one step of a full run, or two steps of the longest run that takes pairs).
 constexpr int kPairS = 4;
 
-// Blocks of rows an LDS tile of a kernel for runs of up to R blocks holds: one step of a
-// full run, and for runs short enough to take pairs, two steps of the longest such run.
 constexpr int tile_blocks(int R) { return R <= kPairS ? 2 * R : R; }
-static_assert(2 * kPairS <= kRunGateUp && 2 * kPairS <= kRunDownShort,
+static_assert(2 * kPairS <= tile_blocks(kRunGateUpShort) && 2 * kPairS <= kRunDownShort &&
+                  2 * kPairS <= kRunGateUp,
               "a pair of steps must fit one LDS tile");
 
 template <int F, int ACT, int SW, int NR, int S>
