@@ -744,8 +744,8 @@ def _down_run(blocks, n_tiles: int, n_cus: int) -> int:
 
 
 def _prefill_work(blocks, run: int, n_tiles: int = 0, n_cus: int = 0):
-    """(work, n_slots, run): the work list of one grouped launch over tables whose experts hold
-    `blocks` 16-row blocks each, in table order. Each expert's blocks form runs of up to
+    """(work, n_slots, run): the work list of one grouped launch over tables whose experts
+    hold `blocks` 16-row blocks each, in table order. Each expert's blocks form runs of up to
     `run` blocks (or the `_run_length` for `n_tiles` N tiles on `n_cus` CUs, when given)
     from its first block on; a run is one work item per N tile, all on one XCD (so they
     share the run's activation rows in its L2). The runs go to the eight XCDs longest
