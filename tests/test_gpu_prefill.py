@@ -358,3 +358,42 @@ def test_the_library_refuses_a_launch_past_its_offset_range():
                                    g, 0, 0, _lib.stream_ptr(buf.device))
     assert rc != 0 and b"32-bit offset" in lib.vaayu_last_error()
     torch.cuda.synchronize()
+
+
+def test_work_entries_that_do_not_fit_the_table_compute_nothing():
+    """The kernels check each work-list entry against the table: a run that reaches past
+    the table's last block, one longer than the launched kernel's run length, and a
+    negative entry compute nothing, while the valid entries' rows come out as from the
+    host's own list."""
+    from vaayu_amd import _lib
+    lib = pk._require_backend()
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, n_exp=3, tokens=200, top_k=2)
+    plan = pk._prefill_plan(eidx)
+    blob = blobs[int(plan[1][0])]
+    geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
+    tbl, rows, _order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
+    ref = pk._gate_up_g(x, tbl, rows, n_blocks, 2, geom, sc, work=work).clone()
+    first_blocks = int((plan[2][0] + 15) // 16)        # the first expert's blocks: 0 ..
+    assert 4 < first_blocks < n_blocks
+    entries = [f * 32 + min(4, first_blocks - f) for f in range(0, first_blocks, 4)]
+    entries += [(n_blocks - 2) * 32 + 3,                # reaches past the last block
+                first_blocks * 32 + 9,                  # longer than the kernel's 4
+                -7]
+    n_slots = -(-len(entries) // 8)
+    bad = torch.full((n_slots * 8,), -1, dtype=torch.int64)
+    bad[:len(entries)] = torch.tensor(entries, dtype=torch.int64)
+    bad = bad.to(x.device)
+    sentinel = torch.tensor(1234.0, dtype=torch.bfloat16)
+    h = torch.full_like(ref, float(sentinel))
+    g = _lib.geom_struct(geom)
+    rc = lib.vaayu_prefill_gate_up(x.data_ptr(), rows.data_ptr(), tbl.data_ptr(),
+                                   bad.data_ptr(), n_slots, 4, h.data_ptr(), n_blocks, 2, g,
+                                   pk._DTYPE_CODE[x.dtype], sc, _lib.stream_ptr(x.device))
+    assert rc == 0, lib.vaayu_last_error()
+    torch.cuda.synchronize()
+    mine = rows[:first_blocks * 16]
+    mine = mine[mine >= 0]
+    assert torch.equal(h[mine], ref[mine])
+    others = torch.ones(h.shape[0], dtype=torch.bool, device=h.device)
+    others[mine] = False
+    assert (h[others] == sentinel.to(h.device)).all()
