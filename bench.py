@@ -451,8 +451,9 @@ def bench_prefill(args, spec):
     prepared = []
     for ei, wi, k in calls:
         plan = pk._prefill_plan(ei)
-        tbl, rows, order, n_blocks, work = pk._prefill_tables(ei, plan, blobs, dev)
-        tbl, rows, order, work = tbl.clone(), rows.clone(), order.clone(), work.clone()
+        tbl, rows, order, n_blocks = pk._prefill_tables(ei, plan, blobs, dev)
+        work = tbl.vaayu_work.clone()                                  # off the table ring
+        tbl, rows, order = tbl.clone(), rows.clone(), order.clone()
         h = torch.empty(T * k, I, dtype=torch.bfloat16, device=dev)
         y = torch.empty(T * k, H, dtype=torch.float32, device=dev)
         out = torch.empty(T, H, dtype=torch.float32, device=dev)

@@ -51,9 +51,9 @@ def _stages(x, eidx, w, blobs, h=None, y=None):
     blob = blobs[int(plan[1][0])]
     geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
     top_k = eidx.shape[1]
-    tbl, rows, order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
-    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=h, work=work)
-    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, y=y, work=work)
+    tbl, rows, order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=h)
+    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, y=y)
     torch.cuda.synchronize()
     return h, y, order, plan
 
@@ -371,8 +371,8 @@ def test_work_entries_that_do_not_fit_the_table_compute_nothing():
     plan = pk._prefill_plan(eidx)
     blob = blobs[int(plan[1][0])]
     geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
-    tbl, rows, _order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
-    ref = pk._gate_up_g(x, tbl, rows, n_blocks, 2, geom, sc, work=work).clone()
+    tbl, rows, _order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    ref = pk._gate_up_g(x, tbl, rows, n_blocks, 2, geom, sc).clone()
     first_blocks = int((plan[2][0] + 15) // 16)        # the first expert's blocks: 0 ..
     assert 4 < first_blocks < n_blocks
     entries = [f * 32 + min(4, first_blocks - f) for f in range(0, first_blocks, 4)]
@@ -397,3 +397,26 @@ def test_work_entries_that_do_not_fit_the_table_compute_nothing():
     others = torch.ones(h.shape[0], dtype=torch.bool, device=h.device)
     others[mine] = False
     assert (h[others] == sentinel.to(h.device)).all()
+
+
+def test_a_table_without_its_work_lists_gets_them_rebuilt():
+    """The reference's call sequence (`_prefill_tables`, then `_gate_up_g` / `_down_g` on
+    its tables) finds the work lists on the table; a copy of the table, which does not
+    carry them, has them rebuilt from its entries, with the same bits (here with experts
+    that share one blob, so consecutive experts have equal table entries)."""
+    x, eidx, w, blobs, _c = prefill_case(*QWEN, n_exp=5, tokens=150, top_k=3)
+    ids = sorted(blobs)
+    blobs = {e: blobs[ids[2 * (i // 2)]] for i, e in enumerate(ids)}   # pairs share a blob
+    plan = pk._prefill_plan(eidx)
+    blob = blobs[int(plan[1][0])]
+    geom, sc = blob["geom"], pk._DTYPE_CODE[blob["flat"]["scale"].dtype]
+    tbl, rows, _order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    assert getattr(tbl, "vaayu_work", None) is not None
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, 3, geom, sc).clone()
+    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc).clone()
+    copy = tbl.clone()
+    assert getattr(copy, "vaayu_work", None) is None
+    h2 = pk._gate_up_g(x, copy, rows, n_blocks, 3, geom, sc)
+    y2 = pk._down_g(h2, copy, rows, n_blocks, w, geom, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(y, y2)

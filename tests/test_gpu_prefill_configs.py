@@ -95,10 +95,9 @@ def _stages(pk, x, eidx, w, blobs):
     blob = blobs[int(plan[1][0])]
     geom, sc = blob["geom"], pk._SCALE_CODE[blob["flat"]["scale"].dtype]
     top_k = eidx.shape[1]
-    tbl, rows, _order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
-    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, work=work)
-    y = pk._down_g(h, tbl, rows, n_blocks, torch.ones(eidx.shape, device=x.device), geom, sc,
-                   work=work)
+    tbl, rows, _order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc)
+    y = pk._down_g(h, tbl, rows, n_blocks, torch.ones(eidx.shape, device=x.device), geom, sc)
     torch.cuda.synchronize()
     return h, y
 

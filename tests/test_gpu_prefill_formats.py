@@ -42,9 +42,9 @@ def _stages(x, eidx, w, blobs):
     plan = pk._prefill_plan(eidx)
     blob = blobs[int(plan[1][0])]
     geom, sc = blob["geom"], pk._SCALE_CODE[blob["flat"]["scale"].dtype]
-    tbl, rows, order, n_blocks, work = pk._prefill_tables(eidx, plan, blobs, x.device)
-    h = pk._gate_up_g(x, tbl, rows, n_blocks, eidx.shape[1], geom, sc, work=work)
-    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc, work=work)
+    tbl, rows, order, n_blocks = pk._prefill_tables(eidx, plan, blobs, x.device)
+    h = pk._gate_up_g(x, tbl, rows, n_blocks, eidx.shape[1], geom, sc)
+    y = pk._down_g(h, tbl, rows, n_blocks, w, geom, sc)
     torch.cuda.synchronize()
     return h, y, order
 

@@ -798,12 +798,15 @@ def _prefill_layout(plan):
 
 def _prefill_tables(eidx_cpu, plan, blobs, device):
     """The call's tables on the device from ONE pinned copy
-    (vaayu/packed_expert_kernels.py:691-717): (tbl, rows, ord, n_blocks, work).
+    (vaayu/packed_expert_kernels.py:691-717): (tbl, rows, ord, n_blocks).
 
     tbl   [n_blocks, 2] (packed address, scale address) of each block's expert
     rows  [n_blocks, _PF_BLOCK_M] row ids, each expert's rows padded to whole blocks with -1
     ord   [tokens, top_k] row ids of each token's slots in ascending expert id
-    work  the gate/up and down launches' work lists (`PrefillWork`, `_prefill_work`)"""
+
+    The gate/up and down launches' work lists (`PrefillWork`, `_prefill_work`) come in the
+    same copy and ride on the returned `tbl` object (`tbl.vaayu_work`), where `_gate_up_g`
+    and `_down_g` find them; a copy of `tbl` does not carry them (see `_work_of`)."""
     _order, live, _counts = plan
     tokens, top_k = eidx_cpu.shape
     lay, blocks, rows = _prefill_layout(plan)
@@ -826,13 +829,39 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     for t in parts:
         at.append(at[-1] + t.numel())
     sl = [dev[at[i]:at[i + 1]] for i in range(len(parts))]
-    return sl[0], sl[1], sl[2], n_blocks, PrefillWork(sl[3], s_gu, sl[4], s_dn, r_dn, r_gu)
+    sl[0].vaayu_work = PrefillWork(sl[3], s_gu, sl[4], s_dn, r_dn, r_gu)
+    return sl[0], sl[1], sl[2], n_blocks
 
 
-def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
+def _work_of(tbl, n_blocks: int, geom) -> PrefillWork:
+    """The work lists of a launch over `tbl`: those `_prefill_tables` attached to it, or,
+    for a table from elsewhere (a copy, a caller's own), lists rebuilt from the table
+    itself (one device-to-host copy): a run only needs its blocks to share one expert's
+    address, which consecutive equal entries give."""
+    work = getattr(tbl, "vaayu_work", None)
+    if work is not None:
+        return work
+    addr = tbl.reshape(-1, 2)[:n_blocks, 0].cpu()
+    change = torch.nonzero(addr[1:] != addr[:-1]).reshape(-1) + 1
+    edges = torch.cat([torch.tensor([0]), change, torch.tensor([n_blocks])])
+    blk = (edges[1:] - edges[:-1]).tolist()
+    lay = _layout(geom)
+    hidden, inter = lay["gate"][3], lay["gate"][2]
+    n_cus = _cu_count(tbl.device)
+    w_gu, s_gu, r_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
+    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus))
+    dev = torch.cat([w_gu, w_dn]).to(tbl.device)
+    work = PrefillWork(dev[:w_gu.numel()], s_gu, dev[w_gu.numel():], s_dn, r_dn, r_gu)
+    tbl.vaayu_work = work
+    return work
+
+
+def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, work=None):
     """h [tokens * top_k, intermediate], activation dtype: SiLU(gate) * up per live row
-    (vaayu/packed_expert_kernels.py:720-732); `work` the call's `PrefillWork`."""
+    (vaayu/packed_expert_kernels.py:720-732); `work` the call's `PrefillWork` (by default
+    `_work_of(tbl)`)."""
     lib = _require_backend()
+    work = work if work is not None else _work_of(tbl, n_blocks, geom)
     g = _lib.geom_struct(geom)
     if h is None:
         h = torch.empty(x.shape[0] * top_k, g.inter, dtype=x.dtype, device=x.device)
@@ -844,10 +873,12 @@ def _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, h=None, *, work):
     return h
 
 
-def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None, *, work):
+def _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, y=None, work=None):
     """y [tokens * top_k, hidden] fp32: each live row's down projection times its weight
-    (vaayu/packed_expert_kernels.py:735-749); `work` the call's `PrefillWork`."""
+    (vaayu/packed_expert_kernels.py:735-749); `work` the call's `PrefillWork` (by default
+    `_work_of(tbl)`)."""
     lib = _require_backend()
+    work = work if work is not None else _work_of(tbl, n_blocks, geom)
     g = _lib.geom_struct(geom)
     rw = routing_weights.reshape(-1).contiguous()
     if y is None:
@@ -887,9 +918,9 @@ def _prefill_call(x, eidx_cpu, routing_weights, blobs, out, plan) -> None:
     blob = blobs[int(plan[1][0])]
     geom, sc, top_k = blob["geom"], _scale_code(blob), eidx_cpu.shape[1]
     x = x.contiguous()
-    tbl, rows, order, n_blocks, work = _prefill_tables(eidx_cpu, plan, blobs, x.device)
-    h = _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc, work=work)
-    y = _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc, work=work)
+    tbl, rows, order, n_blocks = _prefill_tables(eidx_cpu, plan, blobs, x.device)
+    h = _gate_up_g(x, tbl, rows, n_blocks, top_k, geom, sc)
+    y = _down_g(h, tbl, rows, n_blocks, routing_weights, geom, sc)
     dense = out if out.is_contiguous() else torch.empty(out.shape, dtype=torch.float32,
                                                         device=out.device)
     _reduce(y, order, dense, top_k)
