@@ -58,7 +58,7 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i, int dt) {
 // runs, with all N tiles of a run consecutive in that XCD's order, so the items that share
 // a run's activation rows share an L2.
 //
-// Runs of more than 8 blocks (gate/up) take each K step as the MFMAs of the step, then the
+// Runs of more than kPairS blocks take each K step as the MFMAs of the step, then the
 // dequant of the next step's operands, so the two steps' operands are never live together
 // and the 16-block path's 128 accumulators fit two waves per SIMD.
 
@@ -244,49 +244,11 @@ __device__ __forceinline__ BStep b_load(const Role& r, int kc) {
   return o;
 }
 
-// One K step: the MFMAs of this step (rows in `cur`, B operands `o`) with the dequant of
-// the next step's operands (from `raw`, into `on`) spread over them in program order:
-// operand (r, i) of the next step is built after MFMA slot (r*NM + i) * SLOTS / JOBS.
-template <int F, int ACT, int SW, int NR, int S>
-__device__ __forceinline__ void k_step(const char* cur,
-                                       const uint4 (&o)[NR][128 / CodeBits<F>::value / 8],
-                                       const BStep (&raw)[NR], const Role (&role)[NR],
-                                       uint4 (&on)[NR][128 / CodeBits<F>::value / 8],
-                                       const Masks& M, int q, int m, f32x4 (&acc)[NR][S]) {
-  constexpr int CPU = 128 / CodeBits<F>::value;
-  constexpr int NM = CPU / 8;
-  constexpr int KS = 4 * CPU;
-  constexpr int SLOTS = S * NM, JOBS = NR * NM;
-  float sn[NR];
-  GroupK kn[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    sn[r] = applied_scale<F, ACT>(scale_of<SW>(raw[r].s, role[r].bf16_mask));
-    kn[r] = group_of<F>(sn[r]);
-  }
-  // Gate/up reads each A operand two slots before its MFMAs (it feeds two roles, so the read
-  // is worth the registers); down reads it right before (measured: Mixtral down +3 to +7 %
-  // with any read-ahead, gate/up -1 to -3 %).
-  constexpr int AH = NR == 2 ? 2 : 0;
-  uint4 ar[AH + 1];
-#pragma unroll
-  for (int g = 0; g < AH && g < SLOTS; ++g) ar[g] = a_read<KS, S, CPU>(cur, g / NM, g % NM, q, m);
-#pragma unroll
-  for (int g = 0; g < SLOTS; ++g) {
-    const int s = g / NM, i = g % NM;
-    if (g + AH < SLOTS)
-      ar[(g + AH) % (AH + 1)] = a_read<KS, S, CPU>(cur, (g + AH) / NM, (g + AH) % NM, q, m);
-    const uint4 av = ar[g % (AH + 1)];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r][s] = mfma16<ACT>(av, o[r][i], acc[r][s]);
-#pragma unroll
-    for (int j = g * JOBS / SLOTS; j < (g + 1) * JOBS / SLOTS; ++j)
-      on[j / NM][j % NM] = operand_i<F, ACT>(raw[j / NM].q, kn[j / NM], sn[j / NM], M, j % NM);
-  }
-}
-
-// The step of runs longer than 8 blocks: this step's MFMAs first, then the next step's
-// dequant, so the operands of the two steps are never live together.
+// One K step of a run longer than kPairS blocks (rows in `cur`, B operands `o`): this
+// step's MFMAs, each A operand read from LDS two MFMA slots ahead, then the dequant of the
+// next step's operands (from `raw`, into `on`), so the operands of the two steps are never
+// live together. (Measured against the dequant spread between the MFMAs with both operand
+// sets live: the same or faster on every workload, in 60-110 fewer VGPRs.)
 template <int F, int ACT, int SW, int NR, int S>
 __device__ __forceinline__ void k_step_split(const char* cur,
                                              const uint4 (&o)[NR][128 / CodeBits<F>::value / 8],
@@ -460,11 +422,6 @@ __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
   constexpr int KS = 4 * CPU;
   const Masks M = make_masks();
   const int last = K - KS;
-#define KSTEP(...)                                                                    \
-  do {                                                                                \
-    if constexpr (S > 8) k_step_split<F, ACT, SW, NR, S>(__VA_ARGS__);                \
-    else k_step<F, ACT, SW, NR, S>(__VA_ARGS__);                                      \
-  } while (0)
   uint4 oa[NR][NM], ob[NR][NM];
   BStep raw[NR];
 #pragma unroll
@@ -490,21 +447,20 @@ __device__ __forceinline__ void run_k(const Role (&role)[NR], rsrc_t src,
     // scheduling barriers keep the next step's loads ahead of this step's MFMAs
     a_issue<KS, S>(a, src, lds1, k0 + KS);
     __builtin_amdgcn_sched_barrier(0);
-    KSTEP(lds0, oa, raw, role, ob, M, q, m, acc);
+    k_step_split<F, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 2 * KS, last) + q * CPU);
     __syncthreads();
     // step k0 + KS (tile lds1, operands ob) -> step k0 + 2 KS (tile lds0, operands oa)
     a_issue<KS, S>(a, src, lds0, min(k0 + 2 * KS, last));
     __builtin_amdgcn_sched_barrier(0);
-    KSTEP(lds1, ob, raw, role, oa, M, q, m, acc);
+    k_step_split<F, ACT, SW, NR, S>(lds1, ob, raw, role, oa, M, q, m, acc);
 #pragma unroll
     for (int r = 0; r < NR; ++r) raw[r] = b_load<BITS, SW>(role[r], min(k0 + 3 * KS, last) + q * CPU);
     __syncthreads();
   }
   if (k0 < K)                                      // an odd number of steps: the last one
-    KSTEP(lds0, oa, raw, role, ob, M, q, m, acc);
-#undef KSTEP
+    k_step_split<F, ACT, SW, NR, S>(lds0, oa, raw, role, ob, M, q, m, acc);
 }
 
 struct Item {
