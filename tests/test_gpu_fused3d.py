@@ -130,7 +130,7 @@ def test_every_run_length_gives_the_same_bits(monkeypatch):
         monkeypatch.setattr(pk, "_run_length",
                             lambda blocks, run, n_tiles, n_cus, r=r_gu: min(run, r))
         monkeypatch.setattr(pk, "_down_run",
-                            lambda blocks, n_tiles, n_cus, r=r_dn: min(r, max(blocks)))
+                            lambda blocks, n_tiles, n_cus, k=0, r=r_dn: min(r, max(blocks)))
         outs[(r_gu, r_dn)] = mod.forward(x.to(DEV), idx, w.to(DEV)).clone()
     for key, out in outs.items():
         assert torch.equal(out, outs[(8, 8)]), f"runs {key}"

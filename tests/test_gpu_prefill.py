@@ -143,7 +143,7 @@ def test_every_run_length_gives_the_same_bits(monkeypatch):
         monkeypatch.setattr(pk, "_run_length",
                             lambda blocks, run, n_tiles, n_cus, r=r_gu: min(run, r))
         monkeypatch.setattr(pk, "_down_run",
-                            lambda blocks, n_tiles, n_cus, r=r_dn: min(r, max(blocks)))
+                            lambda blocks, n_tiles, n_cus, k=0, r=r_dn: min(r, max(blocks)))
         h, y, _o, _p = _stages(x, eidx, w, blobs)
         outs[(r_gu, r_dn)] = (h.clone(), y.clone())
     h0, y0 = outs[(8, 8)]

@@ -90,12 +90,14 @@ def test_work_lists_spread_the_work_over_the_xcds():
 def test_run_lengths_chosen_per_call():
     """Gate/up: one long expert is cut into runs of 8, so its 2048 rows fill the 256 CUs,
     while a Zipf-routed call keeps runs of 16. Down: the kernel for runs of up to 16 blocks
-    only where it halves the runs (experts of 8-9 blocks), not for Zipf routing."""
+    only where it halves the runs over a long K (experts of 8-9 blocks, K 14336), not for
+    Zipf routing nor a short K."""
     assert pk._run_length([128], 16, 16, 256) == 8
     eidx = _zipf(2048, 256, 8, 0)
     blocks = ((pk._prefill_plan(eidx)[2] + 15) // 16).tolist()
     assert pk._run_length(blocks, 16, 16, 256) == 16
-    assert pk._down_run(blocks, 56, 256) == 8
+    assert pk._down_run(blocks, 56, 256, 2048) == 8
     mixtral = [9, 9, 8, 9, 8, 8, 9, 8]
-    assert pk._down_run(mixtral, 32, 256) == 9
-    assert pk._down_run([1, 2, 1, 3], 16, 256) <= 3
+    assert pk._down_run(mixtral, 32, 256, 14336) == 9
+    assert pk._down_run([16] * 32, 23, 256, 2880) == 8      # gpt-oss-20b: a short K
+    assert pk._down_run([1, 2, 1, 3], 16, 256, 14336) <= 3

@@ -120,7 +120,7 @@ class Fused3DExperts:
         n_cus = pk._cu_count(self.device)
         blk = nblk[lay].tolist()
         w_gu, s_gu, r_gu = pk._prefill_work(blk, pk._run_blocks(0), -(-self.I // 128), n_cus)
-        w_dn, s_dn, r_dn = pk._prefill_work(blk, pk._down_run(blk, -(-self.H // 128), n_cus))
+        w_dn, s_dn, r_dn = pk._prefill_work(blk, pk._down_run(blk, -(-self.H // 128), n_cus, self.I))
         parts = cols + [slot_order, w_gu, w_dn]
         dev = pk._PF_TABLES.put(torch.cat(parts), self.device)
         out, at = [], 0

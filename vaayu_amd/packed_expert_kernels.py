@@ -731,15 +731,18 @@ def _run_length(blocks, run: int, n_tiles: int, n_cus: int) -> int:
     return best
 
 
-def _down_run(blocks, n_tiles: int, n_cus: int) -> int:
-    """The down launch's run length. The library's down kernel for runs of up to 16 blocks
-    holds twice the accumulators of the one for runs of up to 8 (210 VGPRs against 118), so
-    one workgroup runs per CU instead of two: it pays where the longer runs halve the run
-    count (Mixtral's 512-token layer, experts of 8-9 blocks: down 213 -> 175 us) and not
-    where they save little (DeepSeek-V3's Zipf routing: 11 % fewer runs, 1047 -> 1138 us)."""
+def _down_run(blocks, n_tiles: int, n_cus: int, k: int = 0) -> int:
+    """The down launch's run length (k: the down GEMM's K, the intermediate size). The
+    library's down kernel for runs of up to 16 blocks holds twice the accumulators and
+    twice the LDS of the one for runs of up to 8, so one workgroup runs per CU instead of
+    two. It pays only where the longer runs halve the run count over a long K (Mixtral's
+    512-token layer, experts of 8-9 blocks, K 14336: down 185 -> 172 us); not over a short
+    one (gpt-oss-20b, experts of 16 blocks, K 2880: layer 569-576 us with runs of 8 against
+    596-608 us with runs of 16, alternating in one process), nor where they save few runs
+    (DeepSeek-V3's Zipf routing: down 1086 -> 1219 us)."""
     longest = _run_blocks(1)
     runs = {r: sum(-(-int(b) // r) for b in blocks) for r in (8, longest)}
-    run = longest if runs[longest] <= 0.75 * runs[8] else 8
+    run = longest if runs[longest] <= 0.75 * runs[8] and k >= 8192 else 8
     return min(_run_length(blocks, run, n_tiles, n_cus), max(int(b) for b in blocks))
 
 
@@ -822,7 +825,7 @@ def _prefill_tables(eidx_cpu, plan, blobs, device):
     n_cus = _cu_count(device)
     blk = blocks[lay].tolist()
     w_gu, s_gu, r_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
-    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus))
+    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus, inter))
     parts = [tbl, rows, ord_, w_gu, w_dn]
     dev = _PF_TABLES.put(torch.cat(parts), device)
     at = [0]
@@ -849,7 +852,7 @@ def _work_of(tbl, n_blocks: int, geom) -> PrefillWork:
     hidden, inter = lay["gate"][3], lay["gate"][2]
     n_cus = _cu_count(tbl.device)
     w_gu, s_gu, r_gu = _prefill_work(blk, _run_blocks(0), -(-inter // 128), n_cus)
-    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus))
+    w_dn, s_dn, r_dn = _prefill_work(blk, _down_run(blk, -(-hidden // 128), n_cus, inter))
     dev = torch.cat([w_gu, w_dn]).to(tbl.device)
     work = PrefillWork(dev[:w_gu.numel()], s_gu, dev[w_gu.numel():], s_dn, r_dn, r_gu)
     tbl.vaayu_work = work
