@@ -115,13 +115,23 @@ inline const char* rows_out_of_reach(int n_blocks, int top_k, int64_t x_row_byte
 }
 
 // One K step of a run's activation rows (S*16 rows x KS codes, RB = KS*2 bytes a row) lives
-// in LDS as S*16 rows of RB bytes, row r's 16-byte piece c at position c ^ (r % PPR): the
-// A reads of one MFMA (16 rows at one piece) then fall on distinct banks. Rows reach LDS by
+// in LDS as S*16 rows of RB bytes, row r's 16-byte piece c at position c ^ swz(r) (below):
+// the A reads of one MFMA (16 rows at one piece) then fall on distinct banks. Rows reach LDS by
 // direct buffer->LDS loads: one wave instruction writes 1 KB (64 lanes x 16 B) contiguously,
 // i.e. 1024/RB rows, so lane l of instruction g loads row g*(1024/RB) + l/PPR, the piece
 // that belongs at position l % PPR. off[j] is lane's byte offset (at K = 0) in the
 // activation buffer for its j-th instruction g = kWaves*j + wave (kNoRow: a padding row, read as
 // zeros by the bounds check).
+// Row r's 16-byte piece c sits at position c ^ swz(r) of the row. For 16 pieces a row
+// (4-bit codes) the 4x4 transpose of r's low bits keeps the 16 rows an A read touches on
+// distinct banks (SQ_LDS_BANK_CONFLICT: none; with r % 16 two-way conflicts, and down, whose
+// A reads feed one MFMA each, ran up to 12 % slower); 8-bit codes keep r % 8.
+template <int PPR>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (PPR == 16) return ((r >> 2) & 3) | ((r & 3) << 2);
+  else return r % PPR;
+}
+
 template <int KS, int S>
 struct AStage {
   static constexpr int RB = KS * 2;                     // bytes per staged row
@@ -141,7 +151,7 @@ __device__ __forceinline__ void a_plan(AStage<KS, S>& a, RowOff row_off) {
   for (int j = 0; j < A::PER; ++j) {
     const int g = kWaves * j + w;
     const int r = g * A::RPI + l / A::PPR;
-    const int c = (l % A::PPR) ^ (r % A::PPR);
+    const int c = (l % A::PPR) ^ swz<A::PPR>(r);
     const uint32_t ro = g < A::INSTR ? row_off(r) : kNoRow;
     a.off[j] = ro == kNoRow ? kNoRow : ro + c * 16;
   }
@@ -171,7 +181,7 @@ __device__ __forceinline__ uint4 a_read(const char* buf, int s, int i, int q, in
   using A = AStage<KS, S>;
   const int r = s * 16 + m;
   const int piece = q * (CPU / 8) + i;
-  return *(const uint4*)(buf + r * A::RB + ((piece ^ (r % A::PPR)) * 16));
+  return *(const uint4*)(buf + r * A::RB + ((piece ^ swz<A::PPR>(r)) * 16));
 }
 
 // B codes and raw scale bits of one K step for one weight row (lane q's unit).
